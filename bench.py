@@ -1,0 +1,183 @@
+#!/usr/bin/env python3
+"""Benchmark of the INT8 deployment hot path on one MI355X: one Int8Linear forward per step at the FLUX 4K MLP
+up-projection (config c1: M=65536 tokens, K=3072, N=12288, rank-32 low-rank branch, bias, bf16 in/out).
+
+A step is the whole layer on inputs already resident in HBM: low-rank down-projection (t = x @ L1), per-token
+quantizer, fused INT8 GEMM + dequant + low-rank up + bias epilogue. `value` = 2*M*N*K / step time (INT8 TOPS
+of the whole layer). `roofline` prices the dominant kernel (the fused GEMM) against the dense INT8 MFMA peak
+(5.0 POP/s) from HIP events recorded around every GEMM launch of the timed steps, on the stream it runs on.
+`cpu_baseline` times the reference's torch CPU quantize + int-matmul path (restated in oracle/torch_ref.py) on
+a bounded row sample of the same layer.
+
+    python bench.py [--steps K] [--warmup W] [--config c1|c0|c2a|c2b|c3_1280|c3_5120|c4] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0      # dense INT8 MFMA, MI355X (TOP/s)
+METRIC = "INT8 TOPS & % MFMA peak per Int8Linear at FLUX 4K shapes; µs/layer"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c1")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=16384, help="row sample of the CPU baseline")
+    ap.add_argument("--cpu-iters", type=int, default=3)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the INT8 executor "
+              "has no multi-GPU path. Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import CONFIGS, make_linear, make_x, routed_rows
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    lin = make_linear(cfg.K, cfg.N, cfg.lowrank, cfg.bias, dtype=cfg.dtype)
+    q = E.Int8Linear(lin, device=dev, group_size=cfg.group)
+    x = make_x(cfg.M, cfg.K, cfg.dtype).to(dev)
+    rows = routed_rows(dev) if cfg.routed else None
+    M = cfg.M if rows is None else int(rows.numel())
+    canvas = torch.zeros(cfg.M, cfg.N, dtype=cfg.dtype, device=dev) if rows is not None else None
+    out = canvas if canvas is not None else torch.empty(M, cfg.N, dtype=cfg.dtype, device=dev)
+
+    ev = {k: [] for k in ("down", "quant", "gemm")}
+
+    def step(record: bool):
+        def mark():
+            if not record:
+                return None
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            return e
+
+        e0 = mark()
+        t = E.lowrank_down(x, q.lr_At, rows) if q.lr_At is not None else None
+        e1 = mark()
+        xq, sx = E.quant_rows(x, rows)
+        e2 = mark()
+        E._gemm(xq, sx, q.weight_int8, q._scale_k(), q.group_size, q.bias, t, q.lr_Bt, cfg.dtype, out, rows)
+        e3 = mark()
+        if record:
+            if t is not None:
+                ev["down"].append((e0, e1))
+            ev["quant"].append((e1, e2))
+            ev["gemm"].append((e2, e3))
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    def avg_ms(k):
+        v = [a.elapsed_time(b) for a, b in ev[k]]
+        return sum(v) / len(v) if v else 0.0
+
+    ms_step = elapsed / args.steps * 1e3
+    ops = 2.0 * M * cfg.N * cfg.K
+    value = ops / (ms_step * 1e-3) / 1e12
+    gemm_ms = avg_ms("gemm")
+    gemm_tops = ops / (gemm_ms * 1e-3) / 1e12
+    quant_ms = avg_ms("quant")
+    quant_bytes = 3.0 * M * cfg.K + 4.0 * M + (4.0 * M if rows is not None else 0.0)
+    quant_gbs = quant_bytes / (quant_ms * 1e-3) / 1e9
+    down_ms = avg_ms("down")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, lin, args.cpu_rows, args.cpu_iters)
+
+    res = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{cfg.name}: one Int8Linear forward, M={M}, K={cfg.K}, N={cfg.N}, "
+                        f"{'rank-%d low-rank, ' % cfg.lowrank if cfg.lowrank else ''}"
+                        f"{'group-32 weights, ' if cfg.group else 'per-channel weights, '}"
+                        f"{'bias, ' if cfg.bias else ''}{str(cfg.dtype).replace('torch.', '')} in/out"
+                        f"{', routed gather/scatter into a 65536-row canvas' if rows is not None else ''}",
+            "M": M, "K": cfg.K, "N": cfg.N,
+            "us_per_layer": round(ms_step * 1e3, 1),
+            "pct_int8_peak_layer": round(100.0 * value / INT8_PEAK_TOPS, 2),
+            "kernels_us": {"lowrank_down": round(down_ms * 1e3, 1), "quant_rows": round(quant_ms * 1e3, 1),
+                           "int8_gemm": round(gemm_ms * 1e3, 1)},
+            "quant_rows_GBps": round(quant_gbs, 1),
+            "quant_rows_frac_hbm": round(quant_gbs / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(gemm_tops, 2),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
+            "traffic": None,
+            "kernel": "int8_gemm (fused dequant + low-rank + bias epilogue)",
+            "work_per_launch": f"2*M*N*K = {ops:.4e} int8 ops",
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def cpu_baseline(cfg, lin, rows: int, iters: int):
+    """The reference's torch CPU path (oracle/torch_ref.py) on the first `rows` rows of the same layer."""
+    import torch
+
+    from oracle import torch_ref
+    from pyraquant_amd.workloads import make_x
+
+    torch.set_num_threads(min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+    rows = min(rows, cfg.M)
+    x = make_x(cfg.M, cfg.K, cfg.dtype)[:rows].contiguous()
+    wq, ws = torch_ref.quant_weight(lin.weight.detach())
+    b = lin.bias.detach().float() if lin.bias is not None else None
+    from pyraquant_amd.int8_exec import LOWRANK_A_ATTR, LOWRANK_B_ATTR
+
+    A = getattr(lin, LOWRANK_A_ATTR, None)
+    B = getattr(lin, LOWRANK_B_ATTR, None)
+    torch_ref.int8_linear(x, wq, ws, b, A, B)        # warm-up
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        torch_ref.int8_linear(x, wq, ws, b, A, B)
+    dt = (time.perf_counter() - t0) / iters
+    ops = 2.0 * rows * cfg.N * cfg.K
+    return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{rows} of {cfg.M} rows of {cfg.name} (K={cfg.K}, N={cfg.N}), torch CPU quantize + "
+                      f"_int_mm + dequant + low-rank, mean of {iters} after 1 warm-up; "
+                      f"{dt * 1e3:.1f} ms per sample"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

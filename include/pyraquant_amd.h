@@ -1,0 +1,130 @@
+/*
+ * pyraquant_amd.h -- C ABI of libpqint8.so, the MI355X (gfx950) INT8 deployment hot path.
+ *
+ * The library replaces the GPU kernels behind PyraQuant's `Int8Linear` executor
+ * (reference: deploy/int8_exec.py, deploy/run_sdxl_latency.py). Every entry point takes raw device
+ * pointers, element strides and a HIP stream; nothing here allocates or frees device memory, and no
+ * entry point synchronises the stream. All calls are asynchronous on `stream` (pass the caller's
+ * current stream; torch: torch.cuda.current_stream().cuda_stream). The C API keeps no mutable global
+ * state apart from the thread-local error text, so it may be called from several host threads.
+ *
+ * Return value of every int-returning entry point: PQ_OK (0) or a negative PQ_E* code; the text of the
+ * last error on the calling thread is available from pq_last_error().
+ *
+ * Layout contract (all matrices row-major, last dimension contiguous, strides in elements):
+ *   activations x   [M, K]  bf16 or fp16, row stride ldx >= K      (reference: deploy/int8_exec.py:216-230)
+ *   codes       q   [M, K]  int8, contiguous (row stride K)        (reference: deploy/int8_exec.py:225)
+ *   row scales  s   [M]     fp32
+ *   weights     w   [N, K]  int8, row stride ldw (K-contiguous, "TN") (reference: deploy/int8_exec.py:150, 358)
+ *   per-channel scales s_w [N] fp32                                 (reference: deploy/int8_exec.py:356, 359)
+ *   group-32 scales    s_w [K/32, N] fp32 (group-major: one row of N scales per 32-wide K group)
+ *   low-rank down  l1t [R, K] bf16/fp16  = transpose of the reference's lr_A [K, R] (deploy/int8_exec.py:376)
+ *   low-rank up    l2t [N, R] bf16/fp16  = transpose of the reference's lr_B [R, N] (deploy/int8_exec.py:377)
+ *   low-rank mid   t   [M, R] bf16/fp16, row stride ldt             (reference: deploy/int8_exec.py:390)
+ *   output      c   [rows, N] bf16/fp16, row stride ldc
+ */
+#ifndef PYRAQUANT_AMD_H
+#define PYRAQUANT_AMD_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PQ_ABI_VERSION 1
+
+/* status codes */
+#define PQ_OK 0
+#define PQ_EINVAL (-1)  /* null pointer or invalid argument              -> Python AssertionError */
+#define PQ_ESHAPE (-2)  /* unsupported shape (e.g. K % 64 != 0)           -> Python AssertionError */
+#define PQ_EALIGN (-3)  /* pointer / stride alignment not supported       -> Python AssertionError */
+#define PQ_EDTYPE (-4)  /* unsupported dtype code                         -> Python ValueError     */
+#define PQ_ELAUNCH (-5) /* HIP runtime error at launch                    -> Python RuntimeError   */
+
+/* element type codes of the 16-bit floating operands */
+#define PQ_BF16 0
+#define PQ_F16 1
+
+/* Version of this ABI (PQ_ABI_VERSION). No reference counterpart. */
+int pq_abi_version(void);
+
+/* Text of the last error raised on the calling thread ("" if none). No reference counterpart: the
+ * reference reports errors as Python exceptions (deploy/int8_exec.py:67-68, 206, 221, 235). */
+const char* pq_last_error(void);
+
+/*
+ * Per-token activation quantizer, with an optional fused row gather.
+ * Replaces `quant_rows` / `_quant_rows_kernel` (deploy/int8_exec.py:78-101, 216-230) and the SDXL direct
+ * launch `fast_quant_rows` (deploy/run_sdxl_latency.py:159-170).
+ *
+ * For output row m (0 <= m < M) the source row is r = row_idx ? row_idx[m] : m, and
+ *   a    = max(max_k |x[r, k]|, 1e-8f)
+ *   s[m] = a / 127.0f                                    (IEEE fp32 division, round to nearest even)
+ *   q[m, k] = clamp(rint(x[r, k] / s[m]), -127, 127)     (IEEE fp32 division, rint = half to even)
+ * which is the reference's torch restatement (deploy/int8_exec.py:508-509). q is [M, K] contiguous.
+ * row_idx entries must lie in [0, rows of x); they are not range-checked on the device.
+ * Inputs must be finite. Any K >= 1 and ldx >= K are accepted; 16-byte aligned x with ldx % 8 == 0 and
+ * K % 8 == 0 takes the vectorised kernel, anything else a per-element kernel with the same results.
+ */
+int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+                  const int32_t* row_idx, int8_t* q, float* s, hipStream_t stream);
+
+/*
+ * Low-rank down-projection t = x[rows] @ lr_A, fp32 accumulation, rounded to the 16-bit type of x.
+ * Replaces `t = x2.to(self.lr_A.dtype) @ self.lr_A` (deploy/int8_exec.py:390; also :403).
+ * x and l1t must have the same dtype. l1t is lr_A transposed ([R, K], K-contiguous). R % 16 == 0,
+ * R <= 128, K % 8 == 0, 16-byte aligned x / l1t / t, ldx % 8 == 0, ldt % 8 == 0.
+ * row_idx as in pq_quant_rows (the routed gather), or NULL.
+ */
+int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t ldx,
+                    const int32_t* row_idx, const void* l1t, int64_t R, void* t, int64_t ldt,
+                    hipStream_t stream);
+
+/*
+ * Fused INT8 GEMM + dequant epilogue, one kernel. For 0 <= m < M, 0 <= n < N:
+ *   group == 0 : y = (float)(sum_k a[m,k] * w[n,k]) * (s_row[m] * s_w[n])
+ *   group == 32: y = s_row[m] * sum_g s_w[g, n] * (float)(sum_{k in g} a[m,k] * w[n,k])
+ *   if t   : y += sum_r t[m, r] * l2t[n, r]     (fp32 accumulation of the 16-bit operands)
+ *   if bias: y += bias[n]
+ *   c[o, n] = round_to_out_dtype(y), o = out_row_idx ? out_row_idx[m] : m (routed scatter)
+ * The int32 accumulator never leaves registers. Rows of c not named by out_row_idx are not written,
+ * so they keep whatever the caller left there (the routed executor's cached canvas).
+ * Replaces `int8_gemm_fused` / `_int8_gemm_fused_kernel_impl` (deploy/int8_exec.py:144-183, 202-212),
+ * `int8_gemm_lr` / `_int8_gemm_lr_impl` (deploy/int8_exec.py:272-314, 327-336; epilogue order
+ * :303-309), the SDXL narrow-N variant (deploy/run_sdxl_latency.py:131-140, 173-195). The group-32
+ * form and the scatter have no reference kernel (weight semantics: pyraquant/quantizers_weight.py:96-109).
+ * Requirements: K % 64 == 0, N % 64 == 0, M >= 1; a, w 16-byte aligned with lda, ldw % 16 == 0;
+ * c 8-byte aligned with ldc % 4 == 0; t, l2t 16-byte aligned with ldt % 8 == 0, R % 16 == 0, R <= 128;
+ * lr_dtype and out_dtype are PQ_BF16 or PQ_F16; out_row_idx entries unique and in range.
+ */
+int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
+                 const float* s_row, const float* s_w, int64_t group, const float* bias,
+                 const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
+                 void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx,
+                 int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/*
+ * int32 accumulator only: c[m, n] = sum_k a[m, k] * w[n, k] (exact). The bit-exact check of the
+ * MFMA contraction; the same kernel body as pq_int8_gemm. Replaces `torch._int_mm(xq, w_int8.t())`
+ * (deploy/int8_exec.py:259). Requirements as pq_int8_gemm, c 8-byte aligned with ldc % 2 == 0.
+ */
+int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c,
+                     int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/*
+ * Dequant epilogue over a materialised int32 accumulator:
+ *   c[m, n] = round_to_out_dtype((float)acc[m, n] * (s_row[m] * s_col[n]) (+ bias[n])).
+ * Replaces `dequant_epilogue` / `_dequant_epilogue_kernel` (deploy/int8_exec.py:104-127, 233-243).
+ * acc is [M, N] contiguous int32.
+ */
+int pq_dequant_epilogue(const int32_t* acc, const float* s_row, const float* s_col, const float* bias,
+                        void* c, int64_t ldc, int32_t out_dtype, int64_t M, int64_t N,
+                        hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PYRAQUANT_AMD_H */

@@ -1,0 +1,98 @@
+"""ctypes binding of libpqint8.so (include/pyraquant_amd.h).
+
+The library must be built (``python -m pyraquant_amd.build``); there is no fallback: every entry point of
+the package raises if the HIP library is missing. Status codes map to the exception types the reference
+raises for the same conditions (deploy/int8_exec.py:67-68, 206, 221, 235): AssertionError for shapes,
+strides and alignment, ValueError for dtypes, RuntimeError for HIP launch failures.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (loads torch's HIP runtime first, so the library binds to the same one)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpqint8.so")
+
+PQ_OK, PQ_EINVAL, PQ_ESHAPE, PQ_EALIGN, PQ_EDTYPE, PQ_ELAUNCH = 0, -1, -2, -3, -4, -5
+PQ_BF16, PQ_F16 = 0, 1
+ABI_VERSION = 1
+
+# every entry point declared in include/pyraquant_amd.h
+EXPORTS = (
+    "pq_abi_version",
+    "pq_last_error",
+    "pq_quant_rows",
+    "pq_lowrank_down",
+    "pq_int8_gemm",
+    "pq_int8_gemm_i32",
+    "pq_dequant_epilogue",
+)
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+_SIGNATURES = {
+    "pq_abi_version": ([], ctypes.c_int),
+    "pq_last_error": ([], ctypes.c_char_p),
+    "pq_quant_rows": ([_p, _i32, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
+    "pq_lowrank_down": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p], ctypes.c_int),
+    "pq_int8_gemm": ([_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p,
+                      _i64, _i64, _i64, _p], ctypes.c_int),
+    "pq_int8_gemm_i32": ([_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
+    "pq_dequant_epilogue": ([_p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p], ctypes.c_int),
+}
+
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def load():
+    """Load libpqint8.so once (raises LibraryMissing if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissing(
+                f"{LIB_PATH} is not built; run `python -m pyraquant_amd.build` (hipcc, gfx950). "
+                "The INT8 executor has no CPU fallback.")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        v = L.pq_abi_version()
+        if v != ABI_VERSION:
+            raise LibraryMissing(f"libpqint8.so ABI version {v} != expected {ABI_VERSION}; rebuild it")
+        _lib = L
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status == PQ_OK:
+        return
+    msg = f"{what}: {load().pq_last_error().decode(errors='replace')}"
+    if status in (PQ_EINVAL, PQ_ESHAPE, PQ_EALIGN):
+        raise AssertionError(msg)
+    if status == PQ_EDTYPE:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return PQ_BF16
+    if dt == torch.float16:
+        return PQ_F16
+    raise ValueError(f"unsupported 16-bit float dtype {dt} (expected bfloat16 or float16)")
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)

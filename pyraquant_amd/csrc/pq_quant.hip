@@ -1,0 +1,333 @@
+// Per-token INT8 activation quantizer (with the routed row gather), the rank-R low-rank down-projection
+// and the stand-alone dequant epilogue, for gfx950.
+//
+// Quantizer semantics (reference: deploy/int8_exec.py:78-101, torch restatement :508-509):
+//   a = max(max_k |x|, 1e-8f); s = a / 127 (IEEE fp32); q = clamp(rint(x / s), -127, 127) with an IEEE
+//   fp32 division and rint = round half to even.
+// One wavefront owns one row. The row is loaded once with 16-byte loads and kept in registers (CH chunks
+// of 8 elements per lane), so x is read from HBM exactly once. The absmax is a packed-u16 max over the
+// magnitude bits (monotonic in |x| for finite 16-bit floats) and a wave reduction.
+//
+// Exact codes without one IEEE division per element: with c = fl(1/s) and r = fl(x * c),
+// |r - fl(x / s)| <= 3 * 2^-24 * 127 < 2.3e-5, so whenever r is farther than kTieMargin from every
+// half-integer, rint(r) == rint(fl(x / s)). rint(r) comes from the 1.5 * 2^23 magic add (round to nearest
+// even in the fp32 adder), whose low byte is the int8 code. Lanes that land within the margin (about one
+// element in 10^4) redo that element with the correctly rounded division.
+#include "pq_common.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace pq {
+
+namespace {
+
+constexpr float kMagic = 12582912.0f;        // 1.5 * 2^23: x + kMagic rounds x to an integer (|x| < 2^22)
+constexpr float kTieMargin = 6.0e-5f;        // > 2.3e-5 error bound of r, see the header comment
+constexpr float kNearHalf = 0.5f - kTieMargin;
+
+// Code of one element: returns kMagic + q as fp32 (its low byte is the int8 code q).
+__device__ __forceinline__ float code_exact(float x, float s) {
+  float q = rintf(__fdiv_rn(x, s));
+  q = fminf(fmaxf(q, -127.0f), 127.0f);
+  return q + kMagic;
+}
+
+__device__ __forceinline__ uint32_t low_bytes4(float m0, float m1, float m2, float m3) {
+  uint32_t b0 = __float_as_uint(m0) & 0xffu, b1 = __float_as_uint(m1) & 0xffu;
+  uint32_t b2 = __float_as_uint(m2) & 0xffu, b3 = __float_as_uint(m3) & 0xffu;
+  return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
+// Quantize 8 elements held in one 16-byte chunk; returns 8 int8 codes packed in a uint2.
+template <int DT>
+__device__ __forceinline__ v2u quant_chunk(v4u v, float s, float rc) {
+  float f[8];
+  f[0] = lo16_to_f32<DT>(v.x); f[1] = hi16_to_f32<DT>(v.x);
+  f[2] = lo16_to_f32<DT>(v.y); f[3] = hi16_to_f32<DT>(v.y);
+  f[4] = lo16_to_f32<DT>(v.z); f[5] = hi16_to_f32<DT>(v.z);
+  f[6] = lo16_to_f32<DT>(v.w); f[7] = hi16_to_f32<DT>(v.w);
+  float m[8];
+  bool near_tie = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float r = f[i] * rc;
+    m[i] = r + kMagic;
+    const float d = fabsf(r - (m[i] - kMagic));
+    near_tie |= d > kNearHalf;
+  }
+  if (__builtin_expect(near_tie, 0)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float r = f[i] * rc;
+      if (fabsf(r - (m[i] - kMagic)) > kNearHalf) m[i] = code_exact(f[i], s);
+    }
+  }
+  return v2u{low_bytes4(m[0], m[1], m[2], m[3]), low_bytes4(m[4], m[5], m[6], m[7])};
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
+    v = v > o ? v : o;
+  }
+  return v;
+}
+
+// Magnitude bits of a 16-bit float pair -> fp32 of the larger magnitude.
+template <int DT>
+__device__ __forceinline__ float absmax_from_bits(uint32_t mag16) {
+  return lo16_to_f32<DT>(mag16);
+}
+
+// Vectorised quantizer: one wave per row, CH 16-byte chunks per lane, 4 rows per 256-thread block.
+template <int DT, int CH>
+__global__ __launch_bounds__(256) void quant_rows_vec_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
+    int8_t* __restrict__ q, float* __restrict__ s) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
+  const v4u* __restrict__ xr = reinterpret_cast<const v4u*>(x + src * ldx);
+  const int nvec = K >> 3;
+  v4u v[CH];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int idx = c * 64 + lane;
+    v[c] = idx < nvec ? __builtin_nontemporal_load(xr + idx) : v4u{0u, 0u, 0u, 0u};
+  }
+  us2 mx2 = {0, 0};
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, v[c].x & 0x7fff7fffu));
+    mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, v[c].y & 0x7fff7fffu));
+    mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, v[c].z & 0x7fff7fffu));
+    mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, v[c].w & 0x7fff7fffu));
+  }
+  uint32_t mx = mx2.x > mx2.y ? mx2.x : mx2.y;
+  mx = wave_max_u32(mx);
+  const float a = fmaxf(absmax_from_bits<DT>(mx), 1e-8f);
+  const float sc = __fdiv_rn(a, 127.0f);
+  const float rc = __fdiv_rn(1.0f, sc);
+  v2u* __restrict__ qr = reinterpret_cast<v2u*>(q + m * (int64_t)K);
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int idx = c * 64 + lane;
+    if (idx < nvec) qr[idx] = quant_chunk<DT>(v[c], sc, rc);
+  }
+  if (lane == 0) s[m] = sc;
+}
+
+// Per-element quantizer for unaligned rows or odd K: one wave per row, two sweeps over the row.
+template <int DT>
+__global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
+    int8_t* __restrict__ q, float* __restrict__ s) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
+  const uint16_t* __restrict__ xr = x + src * ldx;
+  uint32_t mx = 0;
+  for (int k = lane; k < K; k += 64) {
+    const uint32_t b = xr[k] & 0x7fffu;
+    mx = b > mx ? b : mx;
+  }
+  mx = wave_max_u32(mx);
+  const float a = fmaxf(absmax_from_bits<DT>(mx), 1e-8f);
+  const float sc = __fdiv_rn(a, 127.0f);
+  int8_t* __restrict__ qr = q + m * (int64_t)K;
+  for (int k = lane; k < K; k += 64) {
+    const float f = lo16_to_f32<DT>(xr[k]);
+    qr[k] = (int8_t)(__float_as_uint(code_exact(f, sc)) & 0xffu);
+  }
+  if (lane == 0) s[m] = sc;
+}
+
+template <int DT>
+int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t* row_idx, int8_t* q,
+                 float* s, hipStream_t stream) {
+  const dim3 block(256);
+  const dim3 grid((unsigned)((M + 3) / 4));
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const bool vec = ((uintptr_t)x % 16 == 0) && (ldx % 8 == 0) && (K % 8 == 0) && ((uintptr_t)q % 8 == 0);
+  const int need = (int)((K / 8 + 63) / 64);
+  if (vec && need <= 32) {
+#define PQ_QCASE(C)                                                                                       \
+  if (need <= C) {                                                                                        \
+    hipLaunchKernelGGL((quant_rows_vec_kernel<DT, C>), grid, block, 0, stream, xp, ldx, (int)K, M,        \
+                       row_idx, q, s);                                                                    \
+    return check_launch("quant_rows_vec");                                                                \
+  }
+    PQ_QCASE(1) PQ_QCASE(2) PQ_QCASE(3) PQ_QCASE(4) PQ_QCASE(5) PQ_QCASE(6) PQ_QCASE(8) PQ_QCASE(10)
+    PQ_QCASE(12) PQ_QCASE(16) PQ_QCASE(20) PQ_QCASE(24) PQ_QCASE(32)
+#undef PQ_QCASE
+  }
+  hipLaunchKernelGGL((quant_rows_scalar_kernel<DT>), grid, block, 0, stream, xp, ldx, (int)K, M, row_idx,
+                     q, s);
+  return check_launch("quant_rows_scalar");
+}
+
+// ---- low-rank down-projection t = x[rows] @ L1 (x: [*, ldx], l1t = L1^T: [R, K]) --------------------
+// One wave owns 32 rows and all R output columns; bf16/fp16 MFMA 32x32x16 with fp32 accumulation.
+// Lane l feeds row (l % 32) and the 8-element K slice (l / 32) * 8 of every 16-wide step, for both
+// operands, so the MFMA sums exactly the products x[row, k] * L1[k, col].
+template <int DT, int RB>
+__global__ __launch_bounds__(256) void lowrank_down_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
+    const uint16_t* __restrict__ l1t, uint16_t* __restrict__ t, int64_t ldt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 32;
+  if (r0 >= M) return;
+  int64_t mrow = r0 + (lane & 31);
+  const int64_t mcl = mrow < M ? mrow : M - 1;
+  const int64_t src = row_idx ? (int64_t)row_idx[mcl] : mcl;
+  const uint16_t* __restrict__ xr = x + src * ldx + (lane >> 5) * 8;
+  const uint16_t* __restrict__ lr = l1t + (int64_t)(lane & 31) * K + (lane >> 5) * 8;
+  v16f acc[RB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b) acc[b] = v16f{};
+  const int koff = (lane >> 5) * 8;
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    const bool in = (k0 + koff) < K;
+    const v4u xa = in ? *reinterpret_cast<const v4u*>(xr + k0) : v4u{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      const v4u lb = in ? *reinterpret_cast<const v4u*>(lr + (int64_t)b * 32 * K + k0) : v4u{0u, 0u, 0u, 0u};
+      if constexpr (DT == PQ_BF16) {
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, xa),
+                                                         __builtin_bit_cast(v8bf, lb), acc[b], 0, 0, 0);
+      } else {
+        acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, xa),
+                                                        __builtin_bit_cast(v8h, lb), acc[b], 0, 0, 0);
+      }
+    }
+  }
+  // D[i][j]: i = x row block index 8*(r/4) + 4*(lane/32) + r%4, j = output column (lane % 32).
+#pragma unroll
+  for (int b = 0; b < RB; ++b) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = r0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (row < M) t[row * ldt + b * 32 + (lane & 31)] = (uint16_t)f32_to_16_bits<DT>(acc[b][r]);
+    }
+  }
+}
+
+// ---- dequant epilogue over a materialised int32 accumulator ----------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void dequant_epilogue_kernel(
+    const int32_t* __restrict__ acc, const float* __restrict__ s_row, const float* __restrict__ s_col,
+    const float* __restrict__ bias, uint16_t* __restrict__ c, int64_t ldc, int64_t M, int N) {
+  const int64_t q4 = (int64_t)blockIdx.x * 256 + threadIdx.x;   // index of a 4-column group
+  const int n4 = N >> 2;
+  const int64_t m = q4 / n4;
+  if (m >= M) return;
+  const int n = (int)(q4 - m * n4) * 4;
+  const v4i a = *reinterpret_cast<const v4i*>(acc + m * (int64_t)N + n);
+  const float sr = s_row[m];
+  const v4f sc = *reinterpret_cast<const v4f*>(s_col + n);
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) y[e] = (float)a[e] * (sr * sc[e]);
+  if (bias) {
+    const v4f b = *reinterpret_cast<const v4f*>(bias + n);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = y[e] + b[e];
+  }
+  *reinterpret_cast<v2u*>(c + m * ldc + n) = v2u{pack2<DT>(y[0], y[1]), pack2<DT>(y[2], y[3])};
+}
+
+}  // namespace
+
+// ---- error reporting ---------------------------------------------------------------------------------------
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(PQ_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return PQ_OK;
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" int pq_abi_version(void) { return PQ_ABI_VERSION; }
+
+extern "C" const char* pq_last_error(void) { return pq::g_err; }
+
+extern "C" int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+                             const int32_t* row_idx, int8_t* q, float* s, hipStream_t stream) {
+  if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_rows: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+  if (M == 0) return PQ_OK;
+  if (!x || !q || !s) return set_error(PQ_EINVAL, "pq_quant_rows: null pointer");
+  if (ldx < K) return set_error(PQ_ESHAPE, "pq_quant_rows: ldx=%lld < K=%lld", (long long)ldx, (long long)K);
+  if (K > (1LL << 30) || M > (1LL << 40)) return set_error(PQ_ESHAPE, "pq_quant_rows: shape too large");
+  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16>(x, M, K, ldx, row_idx, q, s, stream);
+  if (x_dtype == PQ_F16) return launch_quant<PQ_F16>(x, M, K, ldx, row_idx, q, s, stream);
+  return set_error(PQ_EDTYPE, "pq_quant_rows: unsupported dtype code %d", (int)x_dtype);
+}
+
+extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t ldx,
+                               const int32_t* row_idx, const void* l1t, int64_t R, void* t, int64_t ldt,
+                               hipStream_t stream) {
+  if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_lowrank_down: bad shape");
+  if (M == 0) return PQ_OK;
+  if (!x || !l1t || !t) return set_error(PQ_EINVAL, "pq_lowrank_down: null pointer");
+  if (R < 32 || R > 128 || R % 32 != 0)
+    return set_error(PQ_ESHAPE, "pq_lowrank_down: rank R=%lld must be 32, 64, 96 or 128", (long long)R);
+  if (K % 8 != 0 || ldx < K || ldx % 8 != 0 || ldt < R || ldt % 8 != 0)
+    return set_error(PQ_ESHAPE, "pq_lowrank_down: need K %% 8 == 0, ldx %% 8 == 0, ldt %% 8 == 0");
+  if ((uintptr_t)x % 16 || (uintptr_t)l1t % 16 || (uintptr_t)t % 16)
+    return set_error(PQ_EALIGN, "pq_lowrank_down: x, l1t, t must be 16-byte aligned");
+  if (dtype != PQ_BF16 && dtype != PQ_F16) return set_error(PQ_EDTYPE, "pq_lowrank_down: bad dtype %d", (int)dtype);
+  const dim3 block(256), grid((unsigned)((M + 127) / 128));
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* lp = static_cast<const uint16_t*>(l1t);
+  uint16_t* tp = static_cast<uint16_t*>(t);
+#define PQ_LRCASE(D, RB)                                                                                    \
+  if (dtype == D && R == RB * 32) {                                                                         \
+    hipLaunchKernelGGL((lowrank_down_kernel<D, RB>), grid, block, 0, stream, xp, ldx, (int)K, M, row_idx,  \
+                       lp, tp, ldt);                                                                        \
+    return check_launch("lowrank_down");                                                                    \
+  }
+  PQ_LRCASE(PQ_BF16, 1) PQ_LRCASE(PQ_BF16, 2) PQ_LRCASE(PQ_BF16, 3) PQ_LRCASE(PQ_BF16, 4)
+  PQ_LRCASE(PQ_F16, 1) PQ_LRCASE(PQ_F16, 2) PQ_LRCASE(PQ_F16, 3) PQ_LRCASE(PQ_F16, 4)
+#undef PQ_LRCASE
+  return set_error(PQ_ESHAPE, "pq_lowrank_down: unsupported rank");
+}
+
+extern "C" int pq_dequant_epilogue(const int32_t* acc, const float* s_row, const float* s_col,
+                                   const float* bias, void* c, int64_t ldc, int32_t out_dtype, int64_t M,
+                                   int64_t N, hipStream_t stream) {
+  if (M < 0 || N < 1) return set_error(PQ_ESHAPE, "pq_dequant_epilogue: bad shape");
+  if (M == 0) return PQ_OK;
+  if (!acc || !s_row || !s_col || !c) return set_error(PQ_EINVAL, "pq_dequant_epilogue: null pointer");
+  if (N % 4 != 0 || ldc < N || ldc % 4 != 0)
+    return set_error(PQ_ESHAPE, "pq_dequant_epilogue: need N %% 4 == 0 and ldc %% 4 == 0");
+  if ((uintptr_t)acc % 16 || (uintptr_t)s_col % 16 || (uintptr_t)c % 8 || (bias && (uintptr_t)bias % 16))
+    return set_error(PQ_EALIGN, "pq_dequant_epilogue: misaligned operand");
+  const int64_t groups = M * (N / 4);
+  const dim3 block(256), grid((unsigned)((groups + 255) / 256));
+  if (out_dtype == PQ_BF16) {
+    hipLaunchKernelGGL((dequant_epilogue_kernel<PQ_BF16>), grid, block, 0, stream, acc, s_row, s_col, bias,
+                       static_cast<uint16_t*>(c), ldc, M, (int)N);
+  } else if (out_dtype == PQ_F16) {
+    hipLaunchKernelGGL((dequant_epilogue_kernel<PQ_F16>), grid, block, 0, stream, acc, s_row, s_col, bias,
+                       static_cast<uint16_t*>(c), ldc, M, (int)N);
+  } else {
+    return set_error(PQ_EDTYPE, "pq_dequant_epilogue: bad dtype %d", (int)out_dtype);
+  }
+  return check_launch("dequant_epilogue");
+}

@@ -1,0 +1,478 @@
+"""INT8 deployment executor for MI355X (gfx950): the `Int8Linear` module API of PyraQuant's
+``deploy/int8_exec.py``, backed by hand-written HIP kernels in ``libpqint8.so``.
+
+Drop-in surface (same names, argument meaning and error types as deploy/int8_exec.py):
+  BACKENDS / DEFAULT_BACKEND / BACKEND / set_backend / get_backend           (:58-74)
+  quant_rows(x2) -> (int8 [M,K], fp32 [M])                                   (:216-230)
+  dequant_epilogue(acc, s_row, s_col, bias, out_dtype)                       (:233-243)
+  int8_linear_2d(x2, w_int8, w_scale, bias, backend=None)                    (:246-261)
+  int8_gemm_fused(xq, s_row, w_int8, w_scale, bias, out_dtype)               (:202-212)
+  int8_gemm_lr(xq, s_row, w_i8, w_scale, bias, t, lb, out_dtype)             (:327-336)
+  LOWRANK_A_ATTR / LOWRANK_B_ATTR, Int8Linear(lin, device=None, lowrank=None) (:341-411)
+  is_bf16_whitelisted, convert_linears_to_int8, warm_kernels                 (:415-474)
+  FLUX_TOKEN_SHAPES, _bench, selftest_and_bench, CLI                         (:478-588)
+Additions for the MI355X build: the routed row gather (``row_idx``) and scatter (``out_row_idx``),
+group-32 weight scales (``group_size=32``), the HIP low-rank down-projection ``lowrank_down`` and the
+int32 accumulator entry ``int8_gemm_i32``.
+
+There is one backend, "hip" (the reference's fused "triton" path; the name "triton" is accepted as an alias
+so existing ``--int8-backend triton`` flags keep working). The reference's "cublas" path (an int32 round
+trip through torch._int_mm) is not provided: set_backend("cublas") raises ValueError.
+
+Every kernel runs on the caller's current stream; nothing synchronises. CPU tensors raise AssertionError
+(as the reference's ``assert x2.is_cuda``); a missing library raises at the first call.
+"""
+from __future__ import annotations
+
+import time
+from typing import Callable, Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+
+# --------------------------------------------------------------------------- backend selection
+BACKENDS = ("hip",)
+DEFAULT_BACKEND = "hip"
+BACKEND = DEFAULT_BACKEND
+_BACKEND_ALIASES = {"hip": "hip", "triton": "hip"}
+
+
+def set_backend(name: str) -> str:
+    """Select the INT8 GEMM backend (deploy/int8_exec.py:64-70). Only the fused HIP path exists."""
+    global BACKEND
+    if name not in _BACKEND_ALIASES:
+        raise ValueError(f"unknown INT8 backend {name!r} (expected one of {BACKENDS}; 'triton' is an alias of 'hip')")
+    BACKEND = _BACKEND_ALIASES[name]
+    return BACKEND
+
+
+def get_backend() -> str:
+    return BACKEND
+
+
+# --------------------------------------------------------------------------- kernel wrappers
+def _check_cuda(*ts):
+    for t in ts:
+        if t is not None:
+            assert t.is_cuda, "the INT8 executor runs on the GPU only (got a CPU tensor)"
+
+
+def _row_index(idx: Optional[torch.Tensor], device) -> Optional[torch.Tensor]:
+    if idx is None:
+        return None
+    assert idx.dtype == torch.int32 and idx.dim() == 1 and idx.is_contiguous(), "row index must be contiguous int32 [M]"
+    assert idx.device == device, "row index must be on the input's device"
+    return idx
+
+
+def quant_rows(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """x2 [rows, K] bf16/fp16 -> (int8 [M, K], fp32 scale [M]), per-row symmetric absmax
+    (deploy/int8_exec.py:216-230). Row-slice views pass without a copy (the kernel takes the row stride).
+    ``row_idx`` (int32 [M]): fused routed gather, output row m quantizes x2[row_idx[m]]."""
+    assert x2.dim() == 2 and x2.is_cuda
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    rows, K = x2.shape
+    ri = _row_index(row_idx, x2.device)
+    M = rows if ri is None else ri.shape[0]
+    q = torch.empty((M, K), dtype=torch.int8, device=x2.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x2.device)
+    L = _lib.load()
+    _lib.check(L.pq_quant_rows(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), _lib.ptr(ri),
+                               _lib.ptr(q), _lib.ptr(s), _lib.stream_of(x2.device)), "quant_rows")
+    return q, s
+
+
+def lowrank_down(x2: torch.Tensor, lr_At: torch.Tensor, row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """t = x2[rows] @ lr_A on the GPU (deploy/int8_exec.py:390), fp32 accumulation, 16-bit result.
+    ``lr_At`` is lr_A transposed, [R, K] contiguous, same dtype as x2."""
+    assert x2.dim() == 2 and x2.is_cuda and lr_At.is_cuda
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    assert lr_At.dtype == x2.dtype, "x2 and lr_A must share a dtype (cast x2 first, as the reference does)"
+    assert lr_At.is_contiguous() and lr_At.shape[1] == x2.shape[1], "lr_At must be [R, K] contiguous"
+    rows, K = x2.shape
+    R = lr_At.shape[0]
+    ri = _row_index(row_idx, x2.device)
+    M = rows if ri is None else ri.shape[0]
+    t = torch.empty((M, R), dtype=x2.dtype, device=x2.device)
+    L = _lib.load()
+    _lib.check(L.pq_lowrank_down(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), _lib.ptr(ri),
+                                 _lib.ptr(lr_At), R, _lib.ptr(t), R, _lib.stream_of(x2.device)), "lowrank_down")
+    return t
+
+
+def dequant_epilogue(acc: torch.Tensor, s_row: torch.Tensor, s_col: torch.Tensor,
+                     bias: Optional[torch.Tensor], out_dtype: torch.dtype) -> torch.Tensor:
+    """int32 [M,N] * s_row[M] * s_col[N] (+bias[N]) -> bf16/fp16 (deploy/int8_exec.py:233-243)."""
+    assert acc.dtype == torch.int32 and acc.is_contiguous()
+    _check_cuda(acc, s_row, s_col, bias)
+    M, N = acc.shape
+    out = torch.empty((M, N), dtype=out_dtype, device=acc.device)
+    L = _lib.load()
+    _lib.check(L.pq_dequant_epilogue(_lib.ptr(acc), _lib.ptr(s_row.contiguous()), _lib.ptr(s_col.contiguous()),
+                                     _lib.ptr(None if bias is None else bias.float().contiguous()), _lib.ptr(out), N,
+                                     _lib.dtype_code(out_dtype), M, N, _lib.stream_of(acc.device)), "dequant_epilogue")
+    return out
+
+
+def _gemm(xq: torch.Tensor, s_row: torch.Tensor, w_int8: torch.Tensor, w_scale_k: torch.Tensor, group: int,
+          bias: Optional[torch.Tensor], t: Optional[torch.Tensor], l2t: Optional[torch.Tensor],
+          out_dtype: torch.dtype, out: Optional[torch.Tensor] = None,
+          out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Core launcher of pq_int8_gemm. w_scale_k is in the kernel layout ([N] or [K/32, N])."""
+    assert xq.dim() == 2 and xq.dtype == torch.int8 and w_int8.dtype == torch.int8
+    _check_cuda(xq, s_row, w_int8, w_scale_k, bias, t, l2t, out, out_row_idx)
+    M, K = xq.shape
+    N = w_int8.shape[0]
+    assert w_int8.shape[1] == K, (tuple(xq.shape), tuple(w_int8.shape))
+    assert xq.stride(1) == 1 and w_int8.stride(1) == 1
+    assert s_row.dtype == torch.float32 and s_row.is_contiguous() and s_row.numel() >= M
+    assert w_scale_k.dtype == torch.float32 and w_scale_k.is_contiguous()
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == N
+    ori = _row_index(out_row_idx, xq.device)
+    if ori is not None:
+        assert ori.shape[0] == M and out is not None, "a scatter needs the destination canvas (out=)"
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=xq.device)
+    assert out.dtype == out_dtype and out.dim() == 2 and out.shape[1] == N and out.stride(1) == 1
+    if ori is None:
+        assert out.shape[0] >= M
+    lr_code, R, ldt = 0, 0, 0
+    if t is not None:
+        assert l2t is not None and t.dtype == l2t.dtype and t.stride(1) == 1 and l2t.is_contiguous()
+        R = t.shape[1]
+        assert l2t.shape == (N, R), (tuple(l2t.shape), (N, R))
+        lr_code, ldt = _lib.dtype_code(t.dtype), t.stride(0)
+    L = _lib.load()
+    _lib.check(L.pq_int8_gemm(_lib.ptr(xq), xq.stride(0), _lib.ptr(w_int8), w_int8.stride(0), _lib.ptr(s_row),
+                              _lib.ptr(w_scale_k), group, _lib.ptr(bias), _lib.ptr(t), ldt, _lib.ptr(l2t), R, lr_code,
+                              _lib.ptr(out), out.stride(0), _lib.dtype_code(out_dtype), _lib.ptr(ori), M, N, K,
+                              _lib.stream_of(xq.device)), "int8_gemm")
+    return out
+
+
+def int8_gemm_fused(xq: torch.Tensor, s_row: torch.Tensor, w_int8: torch.Tensor, w_scale: torch.Tensor,
+                    bias: Optional[torch.Tensor], out_dtype: torch.dtype, *, out: Optional[torch.Tensor] = None,
+                    out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """C = (xq @ w_int8^T) * s_row * w_scale (+bias) -> out_dtype in one kernel (deploy/int8_exec.py:202-212).
+    Requires K % 64 == 0 and N % 64 == 0 (the reference asserts N % 256 == 0; N = 640 of SDXL also runs here).
+    ``out``/``out_row_idx``: write row m into out[out_row_idx[m]] (routed scatter; other rows untouched)."""
+    assert xq.shape[1] % 64 == 0 and w_int8.shape[0] % 64 == 0, (xq.shape[1], w_int8.shape[0])
+    return _gemm(xq, s_row, w_int8, w_scale, 0, bias, None, None, out_dtype, out, out_row_idx)
+
+
+def int8_gemm_lr(xq, s_row, w_i8, w_scale, bias, t, lb, out_dtype, *, lb_t: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None):
+    """int8_gemm_fused + the low-rank up-projection t @ lb in the epilogue (deploy/int8_exec.py:327-336);
+    order: acc*scales, + t@lb, + bias. ``lb`` is lr_B [R, N]; pass ``lb_t`` = lb^T [N, R] contiguous to
+    skip the transpose (Int8Linear keeps it as a buffer)."""
+    if lb_t is None:
+        lb_t = lb.t().contiguous()
+    assert xq.shape[1] % 64 == 0 and w_i8.shape[0] % 64 == 0, (xq.shape[1], w_i8.shape[0])
+    return _gemm(xq, s_row, w_i8, w_scale, 0, bias, t, lb_t, out_dtype, out, out_row_idx)
+
+
+def int8_gemm_i32(xq: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
+    """Exact int32 accumulator xq @ w_int8^T with the same MFMA kernel body (torch._int_mm's role,
+    deploy/int8_exec.py:259)."""
+    assert xq.dim() == 2 and xq.dtype == torch.int8 and w_int8.dtype == torch.int8
+    _check_cuda(xq, w_int8)
+    M, K = xq.shape
+    N = w_int8.shape[0]
+    c = torch.empty((M, N), dtype=torch.int32, device=xq.device)
+    L = _lib.load()
+    _lib.check(L.pq_int8_gemm_i32(_lib.ptr(xq), xq.stride(0), _lib.ptr(w_int8), w_int8.stride(0), _lib.ptr(c), N,
+                                  M, N, K, _lib.stream_of(xq.device)), "int8_gemm_i32")
+    return c
+
+
+def int8_linear_2d(x2: torch.Tensor, w_int8: torch.Tensor, w_scale: torch.Tensor,
+                   bias: Optional[torch.Tensor], backend: Optional[str] = None) -> torch.Tensor:
+    """x2 [M,K] bf16/fp16 -> [M,N] in x2's dtype: quantizer + fused GEMM (deploy/int8_exec.py:246-261)."""
+    if backend is not None:
+        if backend not in _BACKEND_ALIASES:
+            raise ValueError(f"unknown INT8 backend {backend!r}")
+    xq, sx = quant_rows(x2)
+    return int8_gemm_fused(xq, sx, w_int8, w_scale, bias, x2.dtype)
+
+
+# --------------------------------------------------------------------------- weight quantization
+def quantize_weight(w: torch.Tensor, group_size: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Weight RTN on the weight's device, fp32 math.
+    group_size 0: per output channel, s [N] (deploy/int8_exec.py:355-357).
+    group_size g: qdq_weight(w, 8, g) codes and scales, s [N, K/g] (pyraquant/quantizers_weight.py:96-109)."""
+    wf = w.detach().float()
+    N, K = wf.shape
+    if not group_size:
+        s = wf.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+        q = torch.round(wf / s[:, None]).clamp_(-127, 127).to(torch.int8)
+        return q.contiguous(), s.contiguous()
+    assert K % group_size == 0, (K, group_size)
+    wg = wf.reshape(N, K // group_size, group_size)
+    s = wg.abs().amax(dim=-1, keepdim=True).clamp_min(1e-8) / 127.0
+    q = torch.round(wg / s).clamp_(-127, 127).to(torch.int8)
+    return q.reshape(N, K).contiguous(), s.reshape(N, K // group_size).contiguous()
+
+
+# Attribute names under which a weight loader may attach a 16-bit low-rank branch to an nn.Linear
+# before conversion (A: [in_features, r], B: [r, out_features]) -- deploy/int8_exec.py:341-342.
+LOWRANK_A_ATTR = "_lowrank_A"
+LOWRANK_B_ATTR = "_lowrank_B"
+
+
+class Int8Linear(nn.Module):
+    """INT8 stand-in for nn.Linear (deploy/int8_exec.py:345-411): int8 weights (buffers) + per-token dynamic
+    int8 activations through the HIP kernels.
+
+    Buffers as in the reference: ``weight_int8`` [N, K], ``w_scale`` ([N]; [N, K/32] with group_size=32),
+    ``bias`` (fp32) and ``lr_A`` [K, R] / ``lr_B`` [R, N]. Kernel-layout copies: ``lr_At`` [R, K], ``lr_Bt``
+    [N, R] and, for group_size=32, ``w_scale_gn`` [K/32, N]."""
+
+    def __init__(self, lin: nn.Linear, device: Optional[torch.device] = None,
+                 lowrank: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, group_size: int = 0):
+        super().__init__()
+        w = lin.weight.detach()
+        if device is not None:
+            w = w.to(device, non_blocking=False)
+        q, s = quantize_weight(w, group_size)
+        self.group_size = int(group_size)
+        self.register_buffer("weight_int8", q)
+        self.register_buffer("w_scale", s)
+        if group_size:
+            self.register_buffer("w_scale_gn", s.t().contiguous())
+        else:
+            self.w_scale_gn = None
+        if lin.bias is not None:
+            b = lin.bias.detach().float()
+            self.register_buffer("bias", (b.to(device) if device is not None else b).contiguous())
+        else:
+            self.bias = None
+        self.in_features = int(lin.in_features)
+        self.out_features = int(lin.out_features)
+        if lowrank is not None:
+            A, B = lowrank
+        else:
+            A = getattr(lin, LOWRANK_A_ATTR, None)
+            B = getattr(lin, LOWRANK_B_ATTR, None)
+        if A is not None and B is not None:
+            A = A.to(device) if device is not None else A
+            B = B.to(device) if device is not None else B
+            self.register_buffer("lr_A", A.contiguous())
+            self.register_buffer("lr_B", B.contiguous())
+            self.register_buffer("lr_At", A.t().contiguous())
+            self.register_buffer("lr_Bt", B.t().contiguous())
+        else:
+            self.lr_A = None
+            self.lr_B = None
+            self.lr_At = None
+            self.lr_Bt = None
+        del w
+
+    def _scale_k(self) -> torch.Tensor:
+        return self.w_scale_gn if self.group_size else self.w_scale
+
+    def forward(self, x: torch.Tensor, row_idx: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """y = Linear(x) through quantizer (+ low-rank down) + fused GEMM (deploy/int8_exec.py:382-408).
+        Routed use: ``row_idx`` gathers rows of x (2-D x only), ``out``/``out_row_idx`` scatter into a canvas."""
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        if x2.stride(1) != 1:
+            x2 = x2.contiguous()
+        t = None
+        if self.lr_A is not None:
+            xl = x2 if x2.dtype == self.lr_A.dtype else x2.to(self.lr_A.dtype)
+            t = lowrank_down(xl, self.lr_At, row_idx)
+        xq, sx = quant_rows(x2, row_idx)
+        y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, t, self.lr_Bt, x2.dtype,
+                  out, out_row_idx)
+        if out is not None or row_idx is not None:
+            return y
+        return y.reshape(*shape[:-1], self.out_features)
+
+    def extra_repr(self) -> str:
+        g = f"group-{self.group_size}" if self.group_size else "per-channel"
+        lr = f", low-rank r={self.lr_A.shape[1]}" if self.lr_A is not None else ""
+        return f"in={self.in_features}, out={self.out_features}, int8 {g} W / per-token A{lr} (HIP gfx950)"
+
+
+# --------------------------------------------------------------------------- model conversion
+def is_bf16_whitelisted(name: str) -> bool:
+    """SVDQuant-style whitelist + adaLN modulation projections, kept in bf16 (deploy/int8_exec.py:415-421)."""
+    top = name.split(".")[0]
+    if top in ("x_embedder", "context_embedder", "proj_out", "time_text_embed", "norm_out"):
+        return True
+    parts = name.split(".")
+    return len(parts) >= 2 and parts[-1] == "linear" and parts[-2].startswith("norm")
+
+
+def convert_linears_to_int8(model: nn.Module, device: Optional[str] = "cuda",
+                            whitelist: Callable[[str], bool] = is_bf16_whitelisted) -> Dict[str, object]:
+    """Replace the token-level nn.Linear layers by Int8Linear in place (deploy/int8_exec.py:424-445); returns the
+    same statistics dict. A low-rank branch attached under LOWRANK_A_ATTR / LOWRANK_B_ATTR is carried over."""
+    dev = torch.device(device) if device is not None else None
+    n_int8, n_keep, p_int8, p_keep, kept = 0, 0, 0, 0, []
+    targets = [(n, m) for n, m in model.named_modules() if isinstance(m, nn.Linear)]
+    for name, lin in targets:
+        if whitelist(name):
+            n_keep += 1
+            p_keep += lin.weight.numel()
+            kept.append(name)
+            continue
+        parent_name, _, attr = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        setattr(parent, attr, Int8Linear(lin, device=dev))
+        n_int8 += 1
+        p_int8 += lin.weight.numel()
+        del lin
+    if dev is not None and dev.type == "cuda":
+        torch.cuda.synchronize()
+    return {"n_int8_linear": n_int8, "n_bf16_linear_kept": n_keep, "params_int8": p_int8,
+            "params_bf16_linear_kept": p_keep, "bf16_kept_names": kept, "int8_weight_gib": p_int8 / 2**30,
+            "bf16_equiv_gib": p_int8 * 2 / 2**30}
+
+
+# --------------------------------------------------------------------------- warm-up / self-test / micro-benchmark
+FLUX_TOKEN_SHAPES = {   # (K, N): count -- FLUX.1-schnell token-level Linears (deploy/int8_exec.py:478-483)
+    (3072, 3072): 19 * 8 + 38 * 3,
+    (3072, 12288): 19 * 2 + 38,
+    (12288, 3072): 19 * 2,
+    (15360, 3072): 38,
+}
+
+
+def warm_kernels(Ms=(4352, 16640, 65792), device="cuda", lowrank_R=32, warm_lowrank: bool = True):
+    """Signature of deploy/int8_exec.py:448-474. The HIP kernels are compiled ahead of time, so there is no JIT
+    or autotune to pre-pay; this runs every (K, N) shape once at a small M to load the code objects and
+    surface any launch error before a timed region. ``Ms`` is accepted for compatibility."""
+    t0 = time.perf_counter()
+    for (K, N) in FLUX_TOKEN_SHAPES:
+        w = torch.randint(-127, 127, (N, K), device=device, dtype=torch.int8)
+        s = torch.rand(N, device=device)
+        b = torch.rand(N, device=device)
+        x = torch.randn(64, K, device=device, dtype=torch.bfloat16)
+        int8_linear_2d(x, w, s, b)
+        int8_linear_2d(x[:8], w, s, b)
+        if warm_lowrank:
+            lbt = torch.randn(N, lowrank_R, device=device, dtype=torch.bfloat16)
+            lat = torch.randn(lowrank_R, K, device=device, dtype=torch.bfloat16)
+            xq, sx = quant_rows(x)
+            t = lowrank_down(x, lat)
+            _gemm(xq, sx, w, s, 0, b, t, lbt, torch.bfloat16)
+            _gemm(xq, sx, w, s, 0, None, t, lbt, torch.bfloat16)
+    torch.cuda.synchronize()
+    print(f"[int8_exec] kernels warmed (backend={BACKEND}, gemm+lowrank r={lowrank_R}) in "
+          f"{time.perf_counter() - t0:.1f}s", flush=True)
+
+
+def _bench(fn, iters=20, warm=3):
+    """Mean ms per call after ``warm`` calls, synced around the loop (deploy/int8_exec.py:486-492)."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t) / iters * 1e3
+
+
+def selftest_and_bench(Ms=(4352, 16640, 33744, 65792), iters=10):
+    """The reference's GPU self-test and per-shape micro-benchmark (deploy/int8_exec.py:495-571), run on the HIP
+    kernels. Same inputs, same report keys, same assertions."""
+    dev = "cuda"
+    torch.manual_seed(0)
+    lin = nn.Linear(3072, 12288, bias=True).to(dev, torch.bfloat16)
+    x = (torch.randn(4352, 3072, device=dev) * 2).to(torch.bfloat16)
+    x[:, 5] *= 30.0
+    ref_bf16 = F.linear(x, lin.weight, lin.bias).float()
+    q = Int8Linear(lin, device=torch.device(dev))
+    y = q(x).float()
+    xq, sx = quant_rows(x)
+    ref_int8 = (xq.float() @ q.weight_int8.float().t()) * sx[:, None] * q.w_scale[None, :] + q.bias[None, :]
+    xf = x.float()
+    sc = xf.abs().amax(1, keepdim=True).clamp_min(1e-8) / 127
+    xq_ref = torch.round(xf / sc).clamp(-127, 127).to(torch.int8)
+    ref_int8_bf16 = ref_int8.to(torch.bfloat16).float()
+    x_plain = torch.randn(4352, 3072, device=dev).to(torch.bfloat16)
+    y_plain = q(x_plain).float()
+    ref_plain = F.linear(x_plain, lin.weight, lin.bias).float()
+    rep = {
+        "act_quant_mismatch_elems": int((xq != xq_ref).sum().item()),
+        "act_scale_max_rel_err": float(((sx - sc[:, 0]).abs() / sc[:, 0]).max().item()),
+        "fused_vs_unfused_int8_max_abs": float((y - ref_int8_bf16).abs().max().item()),
+        "fused_vs_unfused_int8_rel": float(((y - ref_int8_bf16).norm() / ref_int8_bf16.norm()).item()),
+        "int8_vs_bf16_rel_outlier30x": float(((y - ref_bf16).norm() / ref_bf16.norm()).item()),
+        "int8_vs_bf16_rel_plain": float(((y_plain - ref_plain).norm() / ref_plain.norm()).item()),
+    }
+    xs = x[:8]
+    ys = q(xs).float()
+    qs, ss = quant_rows(xs)
+    rs = ((qs.float() @ q.weight_int8.float().t()) * ss[:, None] * q.w_scale[None, :] + q.bias[None, :]).to(torch.bfloat16).float()
+    rep["smallM_fused_vs_unfused_rel"] = float(((ys - rs).norm() / rs.norm()).item())
+    yt = int8_gemm_fused(xq, sx, q.weight_int8, q.w_scale, q.bias, torch.bfloat16).float()
+    rep["hip_gemm_vs_module_max_abs"] = float((yt - y).abs().max().item())
+    rep["hip_gemm_vs_unfused_rel"] = float(((yt - ref_int8_bf16).norm() / ref_int8_bf16.norm()).item())
+    yts = int8_gemm_fused(qs, ss, q.weight_int8, q.w_scale, q.bias, torch.bfloat16).float()
+    rep["hip_smallM_vs_unfused_rel"] = float(((yts - rs).norm() / rs.norm()).item())
+    x3 = x[:2048].reshape(8, 256, 3072)
+    rep["3d_input_ok"] = bool(torch.equal(q(x3).reshape(2048, -1), q(x[:2048])))
+    print("[int8_exec] selftest:", rep, flush=True)
+    rep["act_quant_mismatch_frac"] = rep["act_quant_mismatch_elems"] / x.numel()
+    assert rep["act_quant_mismatch_frac"] <= 1e-4, rep
+    assert rep["fused_vs_unfused_int8_rel"] < 1e-3 and rep["int8_vs_bf16_rel_plain"] < 2e-2, rep
+    assert rep["hip_gemm_vs_unfused_rel"] < 1e-3 and rep["hip_smallM_vs_unfused_rel"] < 1e-3, rep
+    del lin, q, x, ref_bf16, ref_int8, y, x_plain, y_plain, ref_plain
+    torch.cuda.empty_cache()
+    out = {"selftest": rep, "gpu": torch.cuda.get_device_name(), "per_M": {}}
+    for M in Ms:
+        tot = {"bf16_ms": 0.0, "int8_fused_ms": 0.0, "quant_ms": 0.0, "gemm_fused_ms": 0.0}
+        per_shape = {}
+        for (K, N), cnt in FLUX_TOKEN_SHAPES.items():
+            lin = nn.Linear(K, N, bias=True).to(dev, torch.bfloat16)
+            x = torch.randn(M, K, device=dev, dtype=torch.bfloat16)
+            q = Int8Linear(lin, device=torch.device(dev))
+            b = _bench(lambda: F.linear(x, lin.weight, lin.bias), iters)
+            f = _bench(lambda: q(x), iters)
+            xq, sx = quant_rows(x)
+            qq = _bench(lambda: quant_rows(x), iters)
+            tg = _bench(lambda: int8_gemm_fused(xq, sx, q.weight_int8, q.w_scale, q.bias, torch.bfloat16), iters)
+            per_shape[f"{K}x{N}"] = {"count": cnt, "bf16_ms": round(b, 3), "int8_fused_ms": round(f, 3),
+                                     "quant_ms": round(qq, 3), "gemm_fused_ms": round(tg, 3),
+                                     "speedup": round(b / f, 3)}
+            tot["bf16_ms"] += b * cnt
+            tot["int8_fused_ms"] += f * cnt
+            tot["quant_ms"] += qq * cnt
+            tot["gemm_fused_ms"] += tg * cnt
+            del lin, x, q, xq, sx
+            torch.cuda.empty_cache()
+        tot = {k: round(v, 2) for k, v in tot.items()}
+        tot["speedup_fused_vs_bf16"] = round(tot["bf16_ms"] / tot["int8_fused_ms"], 3)
+        tot["per_shape"] = per_shape
+        out["per_M"][str(M)] = tot
+        print(f"[int8_exec] M={M}: bf16 {tot['bf16_ms']} ms | int8 {tot['int8_fused_ms']} ms "
+              f"(quant {tot['quant_ms']}, gemm {tot['gemm_fused_ms']}) -> x{tot['speedup_fused_vs_bf16']}", flush=True)
+    return out
+
+
+if __name__ == "__main__":
+    import argparse
+    import json
+
+    ap = argparse.ArgumentParser(description="INT8 kernel self-test and micro-benchmark on the FLUX token-level "
+                                             "Linear shapes (needs an MI355X).")
+    ap.add_argument("out", nargs="?", default=None, help="optional JSON path for the results")
+    ap.add_argument("--int8-backend", choices=tuple(_BACKEND_ALIASES), default=DEFAULT_BACKEND)
+    args = ap.parse_args()
+    set_backend(args.int8_backend)
+    res = selftest_and_bench()
+    res["int8_backend"] = BACKEND
+    if args.out:
+        with open(args.out, "w") as fh:
+            json.dump(res, fh, indent=1)
+        print(f"[int8_exec] saved {args.out}")

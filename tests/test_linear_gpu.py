@@ -1,0 +1,186 @@
+"""GPU parity of the Int8Linear module path (quantizer + low-rank down + fused GEMM) against the CPU oracle,
+the routed executor (gather + scatter), the SDXL group-32 module and the reference's own self-test
+(deploy/int8_exec.py:495-536)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import MAX_REL, MEAN_REL, bits, dcode, rel_errors
+
+pytestmark = pytest.mark.gpu
+
+
+
+def _oracle_module(oracle, q, x, row_idx=None, out_dtype=None):
+    """Oracle of Int8Linear.forward from the module's own int8 weights / scales / low-rank buffers."""
+    dt = dcode(x.dtype)
+    l1 = None if q.lr_A is None else bits(q.lr_A)
+    l2 = None if q.lr_B is None else bits(q.lr_B)
+    return oracle.linear(bits(x), dt, q.weight_int8.cpu().numpy(), q.w_scale.cpu().numpy(),
+                         None if q.bias is None else q.bias.cpu().numpy(), q.group_size, l1, l2,
+                         None if row_idx is None else row_idx.cpu().numpy(), out_dtype)
+
+
+def test_weight_rtn_matches_oracle(oracle, cuda):
+    """Per-channel and group-32 weight RTN on the GPU give the oracle's codes and scales bit for bit."""
+    from pyraquant_amd.int8_exec import quantize_weight
+    from pyraquant_amd.workloads import make_weights
+
+    w = make_weights(1280, 640, 0, False)["w"]
+    for group in (0, 32):
+        q, s = quantize_weight(w.to(cuda), group)
+        qo, so = oracle.quant_weight(w.numpy(), group)
+        assert np.array_equal(q.cpu().numpy(), qo)
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K,R", [(1, 3072, 32), (333, 3072, 32), (4096, 3072, 32), (100, 1280, 64),
+                                   (64, 12288, 32), (7, 15360, 96), (70, 1024, 128)])
+def test_lowrank_down(oracle, cuda, M, K, R):
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    x = make_x(M, K, seed=K + M)
+    g = torch.Generator().manual_seed(R)
+    l1 = (torch.randn(K, R, generator=g) * 0.02).to(torch.bfloat16)
+    t = E.lowrank_down(x.to(cuda), l1.t().contiguous().to(cuda))
+    ref_bits = oracle.lowrank_down(bits(x), 0, bits(l1))
+    # fp64 reference of the same product: the 16-bit result is within bf16 rounding of it
+    ref64 = x.double() @ l1.double()
+    got = t.cpu().double()
+    err = (got - ref64).abs() / ref64.abs().clamp_min(1e-3 * ref64.abs().max())
+    assert float(err.max()) <= 1.5e-2, float(err.max())
+    mx, mean = rel_errors(oracle.to_f32(bits(t), 0), oracle.to_f32(ref_bits, 0))
+    assert mx <= MAX_REL * 2 and mean <= MEAN_REL, (mx, mean)
+
+
+@pytest.mark.parametrize("cfg,M", [("c0", 4096), ("c1", 1000), ("c2a", 500), ("c2b", 700)])
+def test_int8linear_flux(oracle, cuda, cfg, M):
+    """Int8Linear with the rank-32 branch: codes / scales bit-exact, output within 1e-2 max / 5e-3 mean
+    relative of the oracle's fp32 result computed from the same codes."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import CONFIGS, make_linear, make_x
+
+    c = CONFIGS[cfg]
+    lin = make_linear(c.K, c.N, c.lowrank, c.bias)
+    q = E.Int8Linear(lin, device=cuda)
+    x = make_x(M, c.K, c.dtype).to(cuda)
+    y = q(x)
+    assert y.dtype == x.dtype and y.shape == (M, c.N)
+    o = _oracle_module(oracle, q, x)
+    xq, sx = E.quant_rows(x)
+    assert np.array_equal(xq.cpu().numpy(), o["q"])
+    assert np.array_equal(sx.cpu().numpy().view(np.uint32), o["s"].view(np.uint32))
+    mx, mean = rel_errors(oracle.to_f32(bits(y), 0), o["y"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
+def test_int8linear_3d_and_views(cuda):
+    """Leading dims are flattened and restored; a 3-D input gives the same result as its 2-D view
+    (deploy/int8_exec.py:530-531); a row-slice input needs no copy."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    lin = make_linear(3072, 3072, 32, True)
+    q = E.Int8Linear(lin, device=cuda)
+    x = make_x(2048, 3072).to(cuda)
+    assert torch.equal(q(x.reshape(8, 256, 3072)).reshape(2048, -1), q(x))
+    big = make_x(64, 3072 + 12288).to(cuda)
+    assert torch.equal(q(big[:, :3072]), q(big[:, :3072].contiguous()))
+
+
+@pytest.mark.parametrize("N", [1280, 5120])
+def test_sdxl_group32_module(oracle, cuda, N):
+    """Config 3 at reduced M: group-32 weights, fp16 activations, no low rank; bit-exact against the oracle."""
+    from pyraquant_amd import sdxl
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    lin = make_linear(1280, N, 0, True)
+    q = sdxl.SdxlInt8Linear(lin, device=cuda, group_size=32)
+    assert q.w_scale.shape == (N, 40)
+    x = make_x(2048, 1280, torch.float16).to(cuda)
+    y = q(x)
+    o = _oracle_module(oracle, q, x)
+    assert np.array_equal(bits(y), o["out"])
+
+
+def test_sdxl_narrow_n(oracle, cuda):
+    """N = 640 (not a multiple of 256) runs on the same kernel (deploy/run_sdxl_latency.py:104-140)."""
+    from pyraquant_amd import sdxl
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    for K, N in sdxl.SDXL_TOKEN_SHAPES[:4]:
+        lin = make_linear(K, N, 0, True)
+        q = sdxl.SdxlInt8Linear(lin, device=cuda)
+        x = make_x(154, K, torch.float16, seed=K).to(cuda)
+        o = _oracle_module(oracle, q, x)
+        assert np.array_equal(bits(q(x)), o["out"])
+
+
+def test_routed_linear_small(oracle, cuda):
+    """Gather + scatter at a reduced canvas: every routed row equals the oracle on the gathered rows, every
+    other canvas row keeps the cached input bits."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.routing import routed_row_index
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    H = W = 64
+    sel = torch.zeros(4, 4, dtype=torch.bool)
+    sel[0, 1] = sel[1, 1] = sel[1, 2] = sel[3, 3] = True
+    rows = routed_row_index(sel, leaf_tokens=16, halo_tokens=2, token_hw=(H, W)).to(cuda)
+    lin = make_linear(3072, 768, 32, True)
+    q = E.Int8Linear(lin, device=cuda)
+    x = make_x(H * W, 3072).to(cuda)
+    cache = make_x(H * W, 768, seed=99).to(cuda)
+    canvas = cache.clone()
+    q(x, row_idx=rows, out=canvas, out_row_idx=rows)
+    o = _oracle_module(oracle, q, x, rows)
+    r = rows.cpu().numpy()
+    got = oracle.to_f32(bits(canvas)[r], 0)
+    mx, mean = rel_errors(got, o["y"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    keep = np.setdiff1d(np.arange(H * W), r)
+    assert np.array_equal(bits(canvas)[keep], bits(cache)[keep])
+
+
+def test_routed_linear_c4_full(oracle, cuda):
+    """Config 4 at full size: 33,316 gathered rows of the 65,536-row canvas. Routed output rows equal the
+    dense Int8Linear output rows bit for bit (row-local math), untouched rows keep the cache, and the codes
+    of the gather equal the oracle's."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x, routed_rows
+
+    lin = make_linear(3072, 12288, 32, True)
+    q = E.Int8Linear(lin, device=cuda)
+    x = make_x(65536, 3072).to(cuda)
+    rows = routed_rows(cuda)
+    cache = torch.full((65536, 12288), 7.0, dtype=torch.bfloat16, device=cuda)
+    canvas = cache.clone()
+    q(x, row_idx=rows, out=canvas, out_row_idx=rows)
+    dense = q(x)
+    ri = rows.long()
+    assert torch.equal(canvas[ri], dense[ri])
+    mask = torch.ones(65536, dtype=torch.bool, device=cuda)
+    mask[ri] = False
+    assert bool((canvas[mask] == 7.0).all())
+    xq, _ = E.quant_rows(x, rows)
+    qo, _ = oracle.quant_rows(bits(x), 0, rows.cpu().numpy())
+    assert np.array_equal(xq.cpu().numpy(), qo)
+
+
+def test_reference_selftest(cuda):
+    """The reference's own GPU self-test assertions (deploy/int8_exec.py:533-536) on the HIP kernels."""
+    from pyraquant_amd import int8_exec as E
+
+    rep = E.selftest_and_bench(Ms=(), iters=1)["selftest"]
+    assert rep["act_quant_mismatch_elems"] == 0
+    assert rep["3d_input_ok"]
+
+
+def test_backend_api():
+    from pyraquant_amd import int8_exec as E
+
+    assert E.set_backend("triton") == "hip" and E.get_backend() == "hip"
+    with pytest.raises(ValueError):
+        E.set_backend("cublas")
+    E.set_backend(E.DEFAULT_BACKEND)
