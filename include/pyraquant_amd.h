@@ -72,6 +72,17 @@ int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t 
                   const int32_t* row_idx, int8_t* q, float* s, hipStream_t stream);
 
 /*
+ * Weight round-to-nearest quantization (one-off, at module conversion). w is [N, K] fp32 with row stride ldw.
+ *   group == 0 : s[n]       = max(max_k |w[n, k]|, 1e-8f) / 127           (IEEE fp32 division)
+ *   group == g : s[n, j]    = max(max_{k in [jg, jg+g)} |w[n, k]|, 1e-8f) / 127   (g divides K)
+ *   q[n, k] = clamp(rint(w[n, k] / s), -127, 127), q [N, K] contiguous, s [N] or [N, K / g] contiguous.
+ * Replaces the weight RTN of `Int8Linear.__init__` (deploy/int8_exec.py:352-357) and, for group > 0, the codes
+ * and scales of `qdq_weight(w, 8, group)` (pyraquant/quantizers_weight.py:96-109).
+ */
+int pq_quant_weight(const float* w, int64_t N, int64_t K, int64_t ldw, int64_t group, int8_t* q, float* s,
+                    hipStream_t stream);
+
+/*
  * Low-rank down-projection t = x[rows] @ lr_A, fp32 accumulation, rounded to the 16-bit type of x.
  * Replaces `t = x2.to(self.lr_A.dtype) @ self.lr_A` (deploy/int8_exec.py:390; also :403).
  * x and l1t must have the same dtype. l1t is lr_A transposed ([R, K], K-contiguous). R % 16 == 0,

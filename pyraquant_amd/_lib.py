@@ -23,6 +23,7 @@ EXPORTS = (
     "pq_abi_version",
     "pq_last_error",
     "pq_quant_rows",
+    "pq_quant_weight",
     "pq_lowrank_down",
     "pq_int8_gemm",
     "pq_int8_gemm_i32",
@@ -37,6 +38,7 @@ _SIGNATURES = {
     "pq_abi_version": ([], ctypes.c_int),
     "pq_last_error": ([], ctypes.c_char_p),
     "pq_quant_rows": ([_p, _i32, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
+    "pq_quant_weight": ([_p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "pq_lowrank_down": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p], ctypes.c_int),
     "pq_int8_gemm": ([_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p,
                       _i64, _i64, _i64, _p], ctypes.c_int),

@@ -5,15 +5,27 @@
 //   group-32   : y[m,n] = s_row[m] * sum_g s_w[g,n] * (float)(sum_{k in g} a[m,k] w[n,k])   (fma over g)
 //   then y += sum_r t[m,r] l2t[n,r] (low-rank up-projection), y += bias[n], rounded to bf16/fp16.
 //
-// Kernel structure. The MFMA computes D = W_tile * A_tile^T: its row operand ("i") is a weight row n and
-// its column operand ("j") an activation row m, so each lane ends up holding 4 consecutive n of one
-// output row m (8-byte bf16 stores) and one s_row value per tile. A workgroup owns a BN x BM output block
-// (n x m), split over a WN x WM grid of wavefronts; each wave holds TI x TJ MFMA tiles of
-// v_mfma_i32_32x32x32_i8 (int32 accumulators, kept in AGPRs). K advances in steps of 64 bytes through an
-// LDS double buffer fed from registers; the 16-byte chunks of every 64-byte LDS row are XOR-swizzled
-// with row bits 1..2 so that the ds_read_b128 of 8 consecutive rows hit 8 different bank groups.
-// Workgroup ids are remapped so that each XCD (ids are dealt round-robin over the 8 XCDs) walks a
-// contiguous run of tiles, rasterised in groups of GROUP_M m-tiles for L2 reuse.
+// Operand roles. The MFMA computes D = W_tile * A_tile^T: its row operand ("i") is a weight row n and its
+// column operand ("j") an activation row m, so each lane ends up holding 4 consecutive n of one output
+// row m (8-byte 16-bit stores) and needs one s_row value per 32 x 32 tile.
+//
+// Per-channel / int32 kernel (gemm_dma_kernel). 256 threads = 2 x 2 wavefronts, one wavefront per SIMD.
+// A workgroup owns a BN x BM (n x m) block, each wave a (BN/2) x (BM/2) quarter held as TI x TJ
+// v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in AGPRs; 256 of them for the 256 x 256 block).
+// K advances in stages of 128 bytes through a two-stage LDS ring filled by LDS-DMA buffer loads
+// (buffer_load_dwordx4 ... lds): no VGPR staging and no ds_write. One DMA instruction fills 1 KB = 8 LDS rows
+// of 128 bytes; each lane fetches the 16-byte chunk that the XOR swizzle places at its LDS slot, so the
+// MFMA operand reads (ds_read_b128, one tile row per lane) are bank-conflict free. Within a stage the four
+// 32-byte K substeps are software-pipelined: the fragments of substep s+1 are read from LDS while the MFMAs
+// of substep s run, and the DMA of stage k+2 is interleaved with the MFMAs of the last substep of stage k.
+// One workgroup barrier per stage.
+//
+// Group-32 kernel (gemm_reg_kernel). Every 32-wide K group is one MFMA whose int32 partial the VALU scales
+// by s_w[g, n] into an fp32 accumulator (VGPRs); K advances in 64-byte stages through a register-staged
+// LDS double buffer.
+//
+// Workgroup ids are remapped so that each XCD (ids are dealt round-robin over the 8 XCDs) walks a contiguous
+// run of tiles, rasterised in groups of GROUP_M m-tiles for L2 reuse.
 #include "pq_common.h"
 
 #include <type_traits>
@@ -21,9 +33,9 @@
 namespace pq {
 namespace {
 
-constexpr int kBK = 64;        // K bytes per pipeline stage
-constexpr int kGroupM = 8;     // m-tiles per raster group
+constexpr int kGroupM = 8;                 // m-tiles per raster group
 constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (raw, 32-bit data format)
+constexpr int kOOB = 0x40000000;           // buffer offset beyond every operand's num_records (loads nothing)
 
 struct GemmArgs {
   const int8_t* a;
@@ -41,6 +53,8 @@ struct GemmArgs {
 };
 
 enum { kModeI32 = 0, kModeChannel = 1, kModeGroup32 = 2 };
+
+typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Map the linear workgroup id to (tile_m, tile_n): XCD-contiguous, then GROUP_M raster.
 __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -65,12 +79,255 @@ __device__ __forceinline__ v16f lr_mfma(v4i a, v4i b, v16f c) {
   }
 }
 
-// Byte offset of 16-byte chunk `chunk` of LDS row `row` (rows of 64 bytes, swizzled).
+// ---- epilogue shared by both kernels ----------------------------------------------------------------------
+// The wave's accumulators cover weight rows nbase + 32 i + [0, 32) and activation rows mbase + 32 j + [0, 32).
+// Lane holds, for tile (i, j) and register r: m = mbase + 32 j + lane % 32,
+// n = nbase + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4. Weight tile outer (its scales / bias / low-rank rows
+// loaded once), rows inner. The fp32 operations run in the reference's order (deploy/int8_exec.py:303-309).
+template <int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT, typename AccT>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, AccT (&acc)[TI][TJ], int nbase, int mbase, int lane) {
+  const int rsub = lane & 31;
+  const int khalf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < TI; ++i) {
+    const int ntile = nbase + i * 32;
+    if (ntile >= p.N) continue;   // N % 32 == 0: a weight tile is entirely in or out of range
+    const int nb = ntile + 4 * khalf;
+    v4f sc[4], bi[4];
+    v4i lb[HAS_LR ? 4 : 1];
+    if constexpr (MODE != kModeI32) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sc[q] = MODE == kModeChannel ? *reinterpret_cast<const v4f*>(p.s_w + nb + 8 * q) : v4f{};
+        bi[q] = p.bias ? *reinterpret_cast<const v4f*>(p.bias + nb + 8 * q) : v4f{};
+      }
+      if constexpr (HAS_LR) {
+        const uint16_t* lrow = p.l2t + (int64_t)(ntile + rsub) * p.R + khalf * 8;
+#pragma unroll
+        for (int rs = 0; rs < 4; ++rs) lb[rs] = rs * 16 < p.R ? *reinterpret_cast<const v4i*>(lrow + rs * 16) : v4i{};
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int m = mbase + j * 32 + rsub;
+      const int mc = min(m, p.M - 1);
+      const bool mvalid = m < p.M;
+      if constexpr (MODE == kModeI32) {
+        if (mvalid) {
+          int32_t* crow = static_cast<int32_t*>(p.c) + (int64_t)m * p.ldc;
+          const v16i& v = acc[i][j];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<v4i*>(crow + nb + 8 * q) = v4i{v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+        }
+      } else {
+        const float sr = p.s_row[mc];
+        float y[16];
+        if constexpr (MODE == kModeChannel) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) y[r] = (float)acc[i][j][r] * (sr * sc[r >> 2][r & 3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) y[r] = acc[i][j][r] * sr;
+        }
+        if constexpr (HAS_LR) {
+          const uint16_t* trow = p.t + (int64_t)mc * p.ldt + khalf * 8;
+          v16f lr = v16f{};
+#pragma unroll
+          for (int rs = 0; rs < 4; ++rs) {
+            if (rs * 16 < p.R) lr = lr_mfma<LRDT>(lb[rs], *reinterpret_cast<const v4i*>(trow + rs * 16), lr);
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) y[r] = y[r] + lr[r];
+        }
+        if (p.bias) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) y[r] = y[r] + bi[r >> 2][r & 3];
+        }
+        if (mvalid) {
+          const int64_t orow = p.out_row_idx ? (int64_t)p.out_row_idx[m] : (int64_t)m;
+          uint16_t* crow = static_cast<uint16_t*>(p.c) + orow * p.ldc;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<v2u*>(crow + nb + 8 * q) =
+                v2u{pack2<ODT>(y[4 * q + 0], y[4 * q + 1]), pack2<ODT>(y[4 * q + 2], y[4 * q + 3])};
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);   // keep one tile's epilogue live at a time (no AGPR mass copy)
+    }
+  }
+}
+
+// ---- per-channel / int32 kernel: LDS-DMA two-stage ring, 128-byte K stages ----------------------------------
+constexpr int kBKd = 128;   // K bytes per stage
+
+// LDS row r (128 bytes, one tile row) stores its 16-byte chunk c at slot c ^ swz(r). Eight consecutive rows put
+// one chunk into eight different slots, and sixteen consecutive rows give sixteen distinct (row parity, slot)
+// pairs, so the ds_read_b128 of 8 (or 16) lanes reading consecutive rows touch distinct banks.
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima). The compiler does not count LDS-DMA loads as
+// LDS writes before a barrier, so every stage hand-over waits for them explicitly.
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
+template <int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
+__global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
+  static_assert(MODE != kModeGroup32, "group-32 runs on gemm_reg_kernel");
+  constexpr int BN = 64 * TI, BM = 64 * TJ;
+  constexpr int WB = BN * kBKd, AB = BM * kBKd, STAGE = WB + AB;
+  constexpr int DW = BN / 32, DA = BM / 32;   // 1 KB DMA instructions per wave and stage (W, A)
+  constexpr int NF = TI + TJ;                 // fragments per substep
+  constexpr int kRest = TI * TJ - NF;         // MFMAs of a substep beyond the NF that carry a fragment read
+  constexpr int kVPer = kRest > 0 ? (DW + DA) / kRest : 0;   // DMA instructions per such MFMA
+  static_assert(DW % 2 == 0 && DA % 2 == 0, "DMA parity assumes an even instruction count");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1;
+  const int wm = wave >> 1;
+
+  int tm, tn;
+  tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+
+  // Buffer resources based at the block's first row. Rows past M / N, and the whole DMA of a stage past the
+  // end of K (offset kOOB), are outside num_records: those loads read no memory.
+  const int rows_w = min(BN, p.N - n0), rows_a = min(BM, p.M - m0);
+  const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.w + (int64_t)n0 * p.ldw), (short)0, (int)(rows_w * p.ldw), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.a + (int64_t)m0 * p.lda), (short)0, (int)(rows_a * p.lda), kBufferWord3);
+
+  // DMA instruction i of this wave fills LDS bytes [(wave * D + i) * 1024, +1024) of its operand tile: rows
+  // (wave * D + i) * 8 + lane / 8, slot lane % 8. The chunk stored at that slot is
+  // (lane % 8) ^ swz(row) = (lane % 8) ^ (lane / 8) ^ (i % 2).
+  const int l8 = lane >> 3;
+  const int ce = ((lane & 7) ^ l8) << 4;
+  const int co = ((lane & 7) ^ l8 ^ 1) << 4;
+  const int vw = (wave * DW * 8 + l8) * (int)p.ldw;
+  const int va = (wave * DA * 8 + l8) * (int)p.lda;
+  const int stw = 8 * (int)p.ldw;
+  const int sta = 8 * (int)p.lda;
+
+  auto dma = [&](int buf, int koff) {
+    uint8_t* sb = smem + buf * STAGE;
+#pragma unroll
+    for (int i = 0; i < DW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, (lds_void_t*)(sb + (wave * DW + i) * 1024), 16,
+                                               vw + i * stw + ((i & 1) ? co : ce) + koff, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < DA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void_t*)(sb + WB + (wave * DA + i) * 1024), 16,
+                                               va + i * sta + ((i & 1) ? co : ce) + koff, 0, 0, 0);
+  };
+
+  // MFMA operand reads: lane reads tile row (lane % 32) of each 32-row fragment, K chunk 2 s + lane / 32 of
+  // substep s. Fragment rows are 32-aligned, so swz(row) depends on the lane only.
+  const int sw = (lane & 7) ^ ((lane >> 3) & 1);
+  const int kh = lane >> 5;
+  const int fw_off = (wn * (BN / 2) + (lane & 31)) * kBKd;
+  const int fa_off = WB + (wm * (BM / 2) + (lane & 31)) * kBKd;
+
+  v16i acc[TI][TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[i][j] = v16i{};
+
+  v4i f0[NF], f1[NF];
+  auto rd = [&](v4i (&f)[NF], int buf, int s) {
+    const uint8_t* sb = smem + buf * STAGE;
+    const int c = ((2 * s + kh) ^ sw) << 4;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) f[i] = *reinterpret_cast<const v4i*>(sb + fw_off + i * 32 * kBKd + c);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) f[TI + j] = *reinterpret_cast<const v4i*>(sb + fa_off + j * 32 * kBKd + c);
+  };
+  auto mm = [&](const v4i (&f)[NF]) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[TI + j], acc[i][j], 0, 0, 0);
+  };
+
+  // Instruction order inside one substep: the NF fragment reads of the next substep are spread over the first NF
+  // MFMAs of this one. In the last substep of a stage the remaining MFMAs also carry the DMA of the stage after
+  // next (issued after the reads: the scheduler keeps LDS reads ahead of a later LDS-DMA it cannot disambiguate).
+  // sched_barrier(0) keeps each substep's MFMAs on its side of the stage barrier.
+  auto interleave = [&](auto with_dma) {
+#pragma unroll
+    for (int q = 0; q < NF; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read
+    }
+    if constexpr (decltype(with_dma)::value && kRest > 0) {
+#pragma unroll
+      for (int q = 0; q < kRest; ++q) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x010, kVPer, 0);     // VMEM (LDS-DMA)
+      }
+    } else if constexpr (kRest > 0) {
+      __builtin_amdgcn_sched_group_barrier(0x008, kRest, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  using no_dma = std::integral_constant<bool, false>;
+  using with_dma = std::integral_constant<bool, true>;
+
+  const int KT = (p.K + kBKd - 1) / kBKd;
+  const bool ktail = (p.K % kBKd) != 0;   // K % 128 == 64: the last stage holds two substeps
+  dma(0, 0);
+  dma(1, KT > 1 ? kBKd : kOOB);
+  wait_dma();
+  __syncthreads();
+  rd(f0, 0, 0);
+  for (int kt = 0; kt < KT - 1; ++kt) {
+    const int b = kt & 1;
+    rd(f1, b, 1);
+    mm(f0);
+    interleave(no_dma{});
+    rd(f0, b, 2);
+    mm(f1);
+    interleave(no_dma{});
+    rd(f1, b, 3);
+    mm(f0);
+    interleave(no_dma{});
+    wait_dma();        // this wave's DMA of stage kt + 1 has landed
+    __syncthreads();   // every wave's has, and every wave is done reading buffer b
+    __builtin_amdgcn_sched_barrier(0);
+    rd(f0, b ^ 1, 0);
+    dma(b, kt + 2 < KT ? (kt + 2) * kBKd : kOOB);
+    mm(f1);
+    interleave(with_dma{});
+  }
+  {
+    const int b = (KT - 1) & 1;
+    rd(f1, b, 1);
+    mm(f0);
+    if (!ktail) {
+      rd(f0, b, 2);
+      mm(f1);
+      rd(f1, b, 3);
+      mm(f0);
+    }
+    mm(f1);
+  }
+
+  epilogue<TI, TJ, MODE, HAS_LR, LRDT, ODT>(p, acc, n0 + wn * (BN / 2), m0 + wm * (BM / 2), lane);
+}
+
+// ---- group-32 kernel: register-staged LDS double buffer, 64-byte K stages ------------------------------------
+constexpr int kBK = 64;   // K bytes per stage
+
+// Byte offset of 16-byte chunk `chunk` of LDS row `row` (rows of 64 bytes, swizzled with row bits 1..2).
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 3)) << 4); }
 
 template <int WN, int WM, int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
 __global__ __attribute__((amdgpu_flat_work_group_size(WN * WM * 64, WN * WM * 64)))
-void gemm_kernel(const GemmArgs p) {
+void gemm_reg_kernel(const GemmArgs p) {
   constexpr int NT = WN * WM * 64;
   constexpr int BN = WN * TI * 32;
   constexpr int BM = WM * TJ * 32;
@@ -92,9 +349,9 @@ void gemm_kernel(const GemmArgs p) {
   const int m0 = tm * BM;
   const int n0 = tn * BN;
 
-  // ---- global -> register loaders. Buffer resources based at the block's first row: rows past M / N
-  //      are outside num_records and load as zeros. Thread owns chunk (tid % 4) of rows
-  //      tid / 4 + ROWS_PER_PASS * i; the per-i and per-stage offsets are wave-uniform (SGPR).
+  // Global -> register loaders. Thread owns chunk (tid % 4) of rows tid / 4 + ROWS_PER_PASS * i; the whole
+  // offset (row, K stage) is in the per-lane voffset, so rows past M / N fall outside num_records and load
+  // as zeros.
   const int lrow = tid >> 2;
   const int lchunk = tid & 3;
   const int rows_w = min(BN, p.N - n0), rows_a = min(BM, p.M - m0);
@@ -109,7 +366,6 @@ void gemm_kernel(const GemmArgs p) {
   const int st_off = lds_off(lrow, lchunk);   // + i * ROWS_PER_PASS * kBK (row bits 1..2 unchanged)
   static_assert((ROWS_PER_PASS & 7) == 0, "rows per pass must keep the swizzle bits");
 
-  // ---- MFMA operand offsets in LDS
   const int rsub = lane & 31;
   const int khalf = lane >> 5;
 
@@ -122,9 +378,9 @@ void gemm_kernel(const GemmArgs p) {
 
   v4i rw[CW], ra[CA];
 #pragma unroll
-  for (int i = 0; i < CW; ++i) rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, vo_w, i * pass_w, 0);
+  for (int i = 0; i < CW; ++i) rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, vo_w + i * pass_w, 0, 0);
 #pragma unroll
-  for (int i = 0; i < CA; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_a, vo_a, i * pass_a, 0);
+  for (int i = 0; i < CA; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_a, vo_a + i * pass_a, 0, 0);
   {
     uint8_t* sw = smem[0];
     uint8_t* sa = smem[0] + BN * kBK;
@@ -142,9 +398,9 @@ void gemm_kernel(const GemmArgs p) {
     if (more) {
       const int ko = (kt + 1) * kBK;
 #pragma unroll
-      for (int i = 0; i < CW; ++i) rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, vo_w, ko + i * pass_w, 0);
+      for (int i = 0; i < CW; ++i) rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, vo_w + ko + i * pass_w, 0, 0);
 #pragma unroll
-      for (int i = 0; i < CA; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_a, vo_a, ko + i * pass_a, 0);
+      for (int i = 0; i < CA; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_a, vo_a + ko + i * pass_a, 0, 0);
     }
     const uint8_t* sw = smem[buf];
     const uint8_t* sa = smem[buf] + BN * kBK;
@@ -199,98 +455,52 @@ void gemm_kernel(const GemmArgs p) {
     __syncthreads();
   }
 
-  // ---- epilogue. Lane holds, for tile (i, j) and register r: m = j-tile row (lane % 32),
-  //      n = 8 * (r / 4) + 4 * (lane / 32) + r % 4 within the 32-row weight tile.
-  //      Loop order: weight tile outer (its scales / bias / low-rank rows loaded once), rows inner.
-#pragma unroll
-  for (int i = 0; i < TI; ++i) {
-    const int ntile = n0 + wn * TI * 32 + i * 32;
-    if (ntile >= p.N) continue;   // N % 32 == 0: a weight tile is entirely in or out of range
-    const int nb = ntile + 4 * khalf;
-    v4f sc[4], bi[4];
-    v4i lb[HAS_LR ? 4 : 1];
-    if constexpr (MODE != kModeI32) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        sc[q] = MODE == kModeChannel ? *reinterpret_cast<const v4f*>(p.s_w + nb + 8 * q) : v4f{};
-        bi[q] = p.bias ? *reinterpret_cast<const v4f*>(p.bias + nb + 8 * q) : v4f{};
-      }
-      if constexpr (HAS_LR) {
-        const uint16_t* lrow = p.l2t + (int64_t)(ntile + rsub) * p.R + khalf * 8;
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs) lb[rs] = rs * 16 < p.R ? *reinterpret_cast<const v4i*>(lrow + rs * 16) : v4i{};
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int m = m0 + wm * TJ * 32 + j * 32 + rsub;
-      const int mc = min(m, p.M - 1);
-      const bool mvalid = m < p.M;
-      if constexpr (MODE == kModeI32) {
-        if (mvalid) {
-          int32_t* crow = static_cast<int32_t*>(p.c) + (int64_t)m * p.ldc;
-          const v16i& v = acc[i][j];
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<v4i*>(crow + nb + 8 * q) = v4i{v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-        }
-      } else {
-        const float sr = p.s_row[mc];
-        float y[16];
-        if constexpr (MODE == kModeChannel) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) y[r] = (float)acc[i][j][r] * (sr * sc[r >> 2][r & 3]);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) y[r] = acc[i][j][r] * sr;
-        }
-        if constexpr (HAS_LR) {
-          const uint16_t* trow = p.t + (int64_t)mc * p.ldt + khalf * 8;
-          v16f lr = v16f{};
-#pragma unroll
-          for (int rs = 0; rs < 4; ++rs) {
-            if (rs * 16 < p.R) lr = lr_mfma<LRDT>(lb[rs], *reinterpret_cast<const v4i*>(trow + rs * 16), lr);
-          }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) y[r] = y[r] + lr[r];
-        }
-        if (p.bias) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) y[r] = y[r] + bi[r >> 2][r & 3];
-        }
-        if (mvalid) {
-          const int64_t orow = p.out_row_idx ? (int64_t)p.out_row_idx[m] : (int64_t)m;
-          uint16_t* crow = static_cast<uint16_t*>(p.c) + orow * p.ldc;
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<v2u*>(crow + nb + 8 * q) =
-                v2u{pack2<ODT>(y[4 * q + 0], y[4 * q + 1]), pack2<ODT>(y[4 * q + 2], y[4 * q + 3])};
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);   // keep one tile's epilogue live at a time (no AGPR mass copy)
-    }
-  }
+  epilogue<TI, TJ, MODE, HAS_LR, LRDT, ODT>(p, acc, n0 + wn * TI * 32, m0 + wm * TJ * 32, lane);
 }
 
-template <int WN, int WM, int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
-int launch(GemmArgs& a, hipStream_t stream) {
-  constexpr int BN = WN * TI * 32, BM = WM * TJ * 32;
+// ---- launchers ---------------------------------------------------------------------------------------------
+int grid_of(GemmArgs& a, int BM, int BN, dim3& grid) {
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
   const int64_t nblocks = (int64_t)a.tiles_m * a.tiles_n;
   if (nblocks > 0x7fffffff) return set_error(PQ_ESHAPE, "pq_int8_gemm: too many tiles");
-  hipLaunchKernelGGL((gemm_kernel<WN, WM, TI, TJ, MODE, HAS_LR, LRDT, ODT>), dim3((unsigned)nblocks),
-                     dim3(WN * WM * 64), 0, stream, a);
+  grid = dim3((unsigned)nblocks);
+  return PQ_OK;
+}
+
+template <int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
+int launch_dma(GemmArgs& a, hipStream_t stream) {
+  dim3 grid;
+  const int st = grid_of(a, 64 * TJ, 64 * TI, grid);
+  if (st != PQ_OK) return st;
+  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, MODE, HAS_LR, LRDT, ODT>), grid, dim3(256), 0, stream, a);
   return check_launch("int8_gemm");
+}
+
+template <int WN, int WM, int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
+int launch_reg(GemmArgs& a, hipStream_t stream) {
+  dim3 grid;
+  const int st = grid_of(a, WM * TJ * 32, WN * TI * 32, grid);
+  if (st != PQ_OK) return st;
+  hipLaunchKernelGGL((gemm_reg_kernel<WN, WM, TI, TJ, MODE, HAS_LR, LRDT, ODT>), grid, dim3(WN * WM * 64), 0,
+                     stream, a);
+  return check_launch("int8_gemm");
+}
+
+// Tile choice of the LDS-DMA kernel: 256 x 256 blocks when they fill the 256 CUs at least twice, else 128 x 128.
+inline bool big_tiles(const GemmArgs& a) {
+  const int64_t t256 = (int64_t)((a.M + 255) / 256) * ((a.N + 255) / 256);
+  return t256 >= 512;
 }
 
 template <int MODE, bool HAS_LR, int LRDT, int ODT>
 int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
   if constexpr (MODE == kModeGroup32) {
     // fp32 accumulators live in VGPRs (the VALU rescales them every group): 2 x 2 waves of 64 x 64
-    return launch<2, 2, 2, 2, MODE, HAS_LR, LRDT, ODT>(a, stream);
+    return launch_reg<2, 2, 2, 2, MODE, HAS_LR, LRDT, ODT>(a, stream);
   } else {
-    return launch<2, 2, 4, 4, MODE, HAS_LR, LRDT, ODT>(a, stream);
+    if (big_tiles(a)) return launch_dma<4, 4, MODE, HAS_LR, LRDT, ODT>(a, stream);
+    return launch_dma<2, 2, MODE, HAS_LR, LRDT, ODT>(a, stream);
   }
 }
 
@@ -318,8 +528,8 @@ int check_common(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int
   if (lda < K || ldw < K) return set_error(PQ_ESHAPE, "%s: lda/ldw < K", who);
   if ((uintptr_t)a % 16 || (uintptr_t)w % 16 || lda % 16 || ldw % 16)
     return set_error(PQ_EALIGN, "%s: a / w must be 16-byte aligned with lda, ldw %% 16 == 0", who);
-  if (256 * lda > 0x7fffffffLL || 256 * ldw > 0x7fffffffLL)   // 32-bit buffer range of one 256-row tile
-    return set_error(PQ_ESHAPE, "%s: row stride too large", who);
+  // every buffer offset of one 256-row tile (row * ld + K offset) must stay below kOOB
+  if (256 * lda + K > kOOB || 256 * ldw + K > kOOB) return set_error(PQ_ESHAPE, "%s: row stride too large", who);
   return PQ_OK;
 }
 
@@ -372,5 +582,6 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
   args.a = a; args.w = w; args.c = c;
   args.lda = lda; args.ldw = ldw; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
-  return launch<2, 2, 4, 4, kModeI32, false, PQ_BF16, PQ_BF16>(args, stream);
+  if (big_tiles(args)) return launch_dma<4, 4, kModeI32, false, PQ_BF16, PQ_BF16>(args, stream);
+  return launch_dma<2, 2, kModeI32, false, PQ_BF16, PQ_BF16>(args, stream);
 }

@@ -216,6 +216,30 @@ __global__ __launch_bounds__(256) void lowrank_down_kernel(
   }
 }
 
+// ---- weight RTN (one-off at conversion) -----------------------------------------------------------------------
+// Per output channel (group == 0, deploy/int8_exec.py:355-357) or per group of `group` consecutive K elements
+// (pyraquant/quantizers_weight.py:96-109): s = max(absmax, 1e-8) / 127 and q = clamp(rint(w / s), -127, 127),
+// both IEEE fp32 divisions. One wave per (row, group) segment; s is [N, K / group] ([N] per channel).
+__global__ __launch_bounds__(256) void quant_weight_kernel(const float* __restrict__ w, int64_t ldw, int N, int K,
+                                                           int group, int8_t* __restrict__ q, float* __restrict__ s) {
+  const int lane = threadIdx.x & 63;
+  const int G = K / group;
+  const int64_t seg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (seg >= (int64_t)N * G) return;
+  const int64_t n = seg / G;
+  const int g = (int)(seg - n * G);
+  const float* __restrict__ wr = w + n * ldw + (int64_t)g * group;
+  float a = 0.0f;
+  for (int k = lane; k < group; k += 64) a = fmaxf(a, fabsf(wr[k]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+  a = fmaxf(a, 1e-8f);
+  const float sc = __fdiv_rn(a, 127.0f);
+  int8_t* __restrict__ qr = q + n * (int64_t)K + (int64_t)g * group;
+  for (int k = lane; k < group; k += 64) qr[k] = (int8_t)(__float_as_uint(code_exact(wr[k], sc)) & 0xffu);
+  if (lane == 0) s[seg] = sc;
+}
+
 // ---- dequant epilogue over a materialised int32 accumulator ----------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(256) void dequant_epilogue_kernel(
@@ -330,4 +354,20 @@ extern "C" int pq_dequant_epilogue(const int32_t* acc, const float* s_row, const
     return set_error(PQ_EDTYPE, "pq_dequant_epilogue: bad dtype %d", (int)out_dtype);
   }
   return check_launch("dequant_epilogue");
+}
+
+extern "C" int pq_quant_weight(const float* w, int64_t N, int64_t K, int64_t ldw, int64_t group, int8_t* q, float* s,
+                               hipStream_t stream) {
+  if (N < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_weight: bad shape N=%lld K=%lld", (long long)N, (long long)K);
+  if (N == 0) return PQ_OK;
+  if (!w || !q || !s) return set_error(PQ_EINVAL, "pq_quant_weight: null pointer");
+  if (ldw < K) return set_error(PQ_ESHAPE, "pq_quant_weight: ldw < K");
+  if (group < 0 || (group > 0 && K % group != 0))
+    return set_error(PQ_ESHAPE, "pq_quant_weight: group %lld must divide K=%lld", (long long)group, (long long)K);
+  if (K > (1LL << 30) || N > (1LL << 30)) return set_error(PQ_ESHAPE, "pq_quant_weight: shape too large");
+  const int g = group ? (int)group : (int)K;
+  const int64_t segs = N * (K / g);
+  hipLaunchKernelGGL(quant_weight_kernel, dim3((unsigned)((segs + 3) / 4)), dim3(256), 0, stream, w, ldw, (int)N,
+                     (int)K, g, q, s);
+  return check_launch("quant_weight");
 }

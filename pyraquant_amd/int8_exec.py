@@ -203,20 +203,22 @@ def int8_linear_2d(x2: torch.Tensor, w_int8: torch.Tensor, w_scale: torch.Tensor
 
 # --------------------------------------------------------------------------- weight quantization
 def quantize_weight(w: torch.Tensor, group_size: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Weight RTN on the weight's device, fp32 math.
+    """Weight RTN on the GPU (pq_quant_weight), fp32 math with IEEE divisions.
     group_size 0: per output channel, s [N] (deploy/int8_exec.py:355-357).
     group_size g: qdq_weight(w, 8, g) codes and scales, s [N, K/g] (pyraquant/quantizers_weight.py:96-109)."""
+    assert w.dim() == 2 and w.is_cuda, "weight quantization runs on the GPU (move the Linear to the device first)"
     wf = w.detach().float()
+    if wf.stride(1) != 1:
+        wf = wf.contiguous()
     N, K = wf.shape
-    if not group_size:
-        s = wf.abs().amax(dim=1).clamp_min(1e-8) / 127.0
-        q = torch.round(wf / s[:, None]).clamp_(-127, 127).to(torch.int8)
-        return q.contiguous(), s.contiguous()
-    assert K % group_size == 0, (K, group_size)
-    wg = wf.reshape(N, K // group_size, group_size)
-    s = wg.abs().amax(dim=-1, keepdim=True).clamp_min(1e-8) / 127.0
-    q = torch.round(wg / s).clamp_(-127, 127).to(torch.int8)
-    return q.reshape(N, K).contiguous(), s.reshape(N, K // group_size).contiguous()
+    if group_size:
+        assert K % group_size == 0, (K, group_size)
+    q = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    s = torch.empty((N, K // group_size) if group_size else (N,), dtype=torch.float32, device=w.device)
+    L = _lib.load()
+    _lib.check(L.pq_quant_weight(_lib.ptr(wf), N, K, wf.stride(0), group_size, _lib.ptr(q), _lib.ptr(s),
+                                 _lib.stream_of(w.device)), "quant_weight")
+    return q, s
 
 
 # Attribute names under which a weight loader may attach a 16-bit low-rank branch to an nn.Linear

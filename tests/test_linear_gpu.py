@@ -173,7 +173,10 @@ def test_reference_selftest(cuda):
     from pyraquant_amd import int8_exec as E
 
     rep = E.selftest_and_bench(Ms=(), iters=1)["selftest"]
-    assert rep["act_quant_mismatch_elems"] == 0
+    # The self-test's reference codes come from torch's GPU ops, whose `amax / 127` by a scalar is a reciprocal
+    # multiply (1-ulp scale differences); its bar is a mismatch fraction <= 1e-4 (deploy/int8_exec.py:533).
+    # Bit-exactness against the IEEE semantics is checked against the CPU oracle in test_quant_gpu.py.
+    assert rep["act_quant_mismatch_frac"] <= 1e-4
     assert rep["3d_input_ok"]
 
 

@@ -120,3 +120,46 @@ def test_quant_rows_routed_c4(oracle, cuda):
     idx = routed_rows(cuda)
     assert idx.numel() == 33316
     _check(oracle, x, idx)
+
+
+@pytest.mark.parametrize("fixture", ["quant_bf16.npz", "quant_f16.npz"])
+def test_quant_rows_golden_fixture(cuda, fixture):
+    """The HIP quantizer reproduces the committed golden vectors (torch CPU, deploy/int8_exec.py:508-509)."""
+    import os
+
+    from pyraquant_amd import int8_exec as E
+
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", fixture), allow_pickle=False)
+    dt = torch.bfloat16 if int(f["dtype"]) == 0 else torch.float16
+    x = torch.from_numpy(f["x_bits"].view(np.int16)).view(dt).to(cuda)
+    q, s = E.quant_rows(x)
+    assert np.array_equal(q.cpu().numpy(), f["q"])
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), f["s"].view(np.uint32))
+
+
+def test_linear_golden_fixture(cuda):
+    """Golden layer (tests/golden/linear_lr.npz): codes, int32 accumulator and no-low-rank fp32 epilogue
+    bit-exact, low-rank output within the tolerance of the float64 value."""
+    import os
+
+    from conftest import MAX_REL, MEAN_REL, rel_errors
+    from pyraquant_amd import int8_exec as E
+
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "linear_lr.npz"), allow_pickle=False)
+    x = torch.from_numpy(f["x_bits"].view(np.int16)).view(torch.bfloat16).to(cuda)
+    wq = torch.from_numpy(f["w_q"]).to(cuda)
+    ws = torch.from_numpy(f["w_s"]).to(cuda)
+    b = torch.from_numpy(f["bias"]).to(cuda)
+    l1 = torch.from_numpy(f["l1_bits"].view(np.int16)).view(torch.bfloat16)
+    l2 = torch.from_numpy(f["l2_bits"].view(np.int16)).view(torch.bfloat16)
+    q, s = E.quant_rows(x)
+    assert np.array_equal(q.cpu().numpy(), f["q"])
+    acc = E.int8_gemm_i32(q, wq)
+    assert np.array_equal(acc.cpu().numpy(), f["acc"])
+    y = E.int8_gemm_fused(q, s, wq, ws, b, torch.bfloat16)
+    ref = torch.from_numpy(f["y_nolr"]).to(torch.bfloat16)
+    assert torch.equal(y.cpu(), ref)
+    t = E.lowrank_down(x, l1.t().contiguous().to(cuda))
+    ylr = E.int8_gemm_lr(q, s, wq, ws, b, t, l2.to(cuda), torch.bfloat16)
+    mx, mean = rel_errors(ylr.float().cpu().numpy(), f["y_lr_f64"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
