@@ -2,8 +2,9 @@
 """Benchmark of the INT8 deployment hot path on one MI355X: one Int8Linear forward per step at the FLUX 4K MLP
 up-projection (config c1: M=65536 tokens, K=3072, N=12288, rank-32 low-rank branch, bias, bf16 in/out).
 
-A step is the whole layer on inputs already resident in HBM: low-rank down-projection (t = x @ L1), per-token
-quantizer, fused INT8 GEMM + dequant + low-rank up + bias epilogue. `value` = 2*M*N*K / step time (INT8 TOPS
+A step is the whole layer on inputs already resident in HBM, as Int8Linear.forward runs it: low-rank
+down-projection (t = x @ L1), per-token quantizer writing packed K64 codes, fused INT8 GEMM over packed operands
++ dequant + low-rank up + bias epilogue (group-32 layers: row-major quantizer and GEMM). `value` = 2*M*N*K / step time (INT8 TOPS
 of the whole layer). `roofline` prices the dominant kernel (the fused GEMM) against the dense INT8 MFMA peak
 (5.0 POP/s) from HIP events recorded around every GEMM launch of the timed steps, on the stream it runs on.
 `cpu_baseline` times the reference's torch CPU quantize + int-matmul path (restated in oracle/torch_ref.py) on
@@ -71,9 +72,15 @@ def main() -> int:
         e0 = mark()
         t = E.lowrank_down(x, q.lr_At, rows) if q.lr_At is not None else None
         e1 = mark()
-        xq, sx = E.quant_rows(x, rows)
-        e2 = mark()
-        E._gemm(xq, sx, q.weight_int8, q._scale_k(), q.group_size, q.bias, t, q.lr_Bt, cfg.dtype, out, rows)
+        if q.weight_packed is not None:
+            xq, sx = E.quant_rows_packed(x, rows)
+            e2 = mark()
+            E.int8_gemm_packed(xq, sx, q.weight_packed, q.w_scale, q.bias, M, cfg.N, cfg.K, cfg.dtype, t=t,
+                               l2t=q.lr_Bt, out=out, out_row_idx=rows)
+        else:
+            xq, sx = E.quant_rows(x, rows)
+            e2 = mark()
+            E._gemm(xq, sx, q.weight_int8, q._scale_k(), q.group_size, q.bias, t, q.lr_Bt, cfg.dtype, out, rows)
         e3 = mark()
         if record:
             if t is not None:

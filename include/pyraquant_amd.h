@@ -22,6 +22,14 @@
  *   low-rank up    l2t [N, R] bf16/fp16  = transpose of the reference's lr_B [R, N] (deploy/int8_exec.py:377)
  *   low-rank mid   t   [M, R] bf16/fp16, row stride ldt             (reference: deploy/int8_exec.py:390)
  *   output      c   [rows, N] bf16/fp16, row stride ldc
+ *
+ * Packed K64 layout (pq_pack_k64, pq_quant_rows_packed, pq_int8_gemm_packed) of an int8 matrix X [R, K], K % 64 == 0:
+ * KT = K / 64 and RB = ceil(R / 16) blocks of 1024 bytes per row block; block (rb, kt) sits at byte offset
+ * (rb * KT + kt) * 1024 and holds rows 16 rb .. 16 rb + 15, bytes 64 kt .. 64 kt + 63 of each. Row r' (= r % 16)
+ * occupies bytes [64 r', 64 r' + 64) of the block and stores its 16-byte chunk c (bytes 64 kt + 16 c ..) at slot
+ * c ^ swz(r'), swz(r') = ((r' >> 2) & 1) | ((((r' >> 1) ^ (r' >> 3)) & 1) << 1). Size RB * KT * 1024 bytes; rows
+ * past R in the last block are zero. A block is the exact LDS image the GEMM's MFMA operand reads expect, so the
+ * GEMM moves it with one 1 KB LDS-DMA per wave and every request is a whole 128-byte line.
  */
 #ifndef PYRAQUANT_AMD_H
 #define PYRAQUANT_AMD_H
@@ -43,9 +51,10 @@ extern "C" {
 #define PQ_EDTYPE (-4)  /* unsupported dtype code                         -> Python ValueError     */
 #define PQ_ELAUNCH (-5) /* HIP runtime error at launch                    -> Python RuntimeError   */
 
-/* element type codes of the 16-bit floating operands */
+/* element type codes of the 16-bit floating operands (and, for pq_int8_gemm_packed's output, raw int32) */
 #define PQ_BF16 0
 #define PQ_F16 1
+#define PQ_I32 2
 
 /* Version of this ABI (PQ_ABI_VERSION). No reference counterpart. */
 int pq_abi_version(void);
@@ -123,6 +132,36 @@ int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
  */
 int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c,
                      int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/*
+ * Fused INT8 GEMM over packed K64 operands (ap: activation codes [M, K], wp: weights [N, K], both in the packed
+ * K64 layout). Same math, epilogue, scatter and requirements as pq_int8_gemm with group == 0; with
+ * out_dtype == PQ_I32, c receives the raw int32 accumulator (s_row, s_w, bias, t, l2t, out_row_idx ignored;
+ * c 16-byte aligned, ldc % 4 == 0). This is the layer path of Int8Linear: the quantizer writes ap directly
+ * (pq_quant_rows_packed) and the weights are packed once at conversion (pq_pack_k64).
+ * Replaces `int8_gemm_fused` / `int8_gemm_lr` (deploy/int8_exec.py:202-212, 327-336) as called from
+ * `Int8Linear.forward` (deploy/int8_exec.py:382-393).
+ */
+int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
+                        const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
+                        void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t M, int64_t N,
+                        int64_t K, hipStream_t stream);
+
+/*
+ * Repack a row-major int8 matrix src [R, K] (row stride lds, K % 64 == 0) into the packed K64 layout at dst
+ * (ceil(R / 16) * 16 * K bytes, 16-byte aligned); padding rows are written as zeros. One-off at weight
+ * conversion. No reference counterpart (the reference's Triton GEMM reads W_int8 row-major,
+ * deploy/int8_exec.py:165-166).
+ */
+int pq_pack_k64(const int8_t* src, int64_t R, int64_t K, int64_t lds, int8_t* dst, hipStream_t stream);
+
+/*
+ * Per-token quantizer writing the codes in the packed K64 layout (qp: ceil(M / 16) * 16 * K bytes, 16-byte
+ * aligned; padding rows zero) instead of row-major; s and every other argument as pq_quant_rows. K % 64 == 0.
+ * Replaces `quant_rows` (deploy/int8_exec.py:216-230) on the Int8Linear forward path (:391).
+ */
+int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+                         const int32_t* row_idx, int8_t* qp, float* s, hipStream_t stream);
 
 /*
  * Dequant epilogue over a materialised int32 accumulator:

@@ -201,3 +201,43 @@ def route_rows_union(mask: np.ndarray, leaf: int = 16, halo: int = 2) -> np.ndar
     rows = np.empty((n,), np.int32)
     lib().pqo_route_rows_union(_ptr(m), gh, gw, leaf, halo, _ptr(rows))
     return rows
+
+
+# ---------------------------------------------------------------------------------------- packed K64 layout
+def k64_swz(r: np.ndarray) -> np.ndarray:
+    """Slot permutation of the packed K64 layout (include/pyraquant_amd.h): bit 0 = bit 2 of r, bit 1 = bit 1 xor
+    bit 3 of r."""
+    r = np.asarray(r)
+    return ((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1)
+
+
+def pack_k64(x: np.ndarray) -> np.ndarray:
+    """Row-major int8 [R, K] -> packed K64 bytes (ceil(R / 16) * 16 * K), restated from the layout's definition:
+    block (rb, kt) at (rb * KT + kt) * 1024, row r' = r % 16 at 64 r', chunk c at slot c ^ swz(r'); padding rows 0.
+    Layout of this build (no reference counterpart); used to check pq_pack_k64 / pq_quant_rows_packed."""
+    x = _c(x, np.int8)
+    R, K = x.shape
+    if K % 64:
+        raise ValueError("K must be a multiple of 64")
+    RB, KT = (R + 15) // 16, K // 64
+    xp = np.zeros((RB * 16, K), np.int8)
+    xp[:R] = x
+    # [RB, 16, KT, 4, 16] -> blocks [RB, KT, 16 rows, 4 slots, 16 bytes]
+    v = xp.reshape(RB, 16, KT, 4, 16).transpose(0, 2, 1, 3, 4)
+    out = np.empty_like(v)
+    rows = np.arange(16)
+    for c in range(4):
+        slot = c ^ k64_swz(rows)                       # [16]
+        out[:, :, rows, slot, :] = v[:, :, rows, c, :]
+    return out.reshape(-1)
+
+
+def unpack_k64(p: np.ndarray, R: int, K: int) -> np.ndarray:
+    """Inverse of pack_k64 (the first R rows)."""
+    RB, KT = (R + 15) // 16, K // 64
+    v = _c(p, np.int8).reshape(RB, KT, 16, 4, 16)
+    out = np.empty_like(v)
+    rows = np.arange(16)
+    for c in range(4):
+        out[:, :, rows, c, :] = v[:, :, rows, c ^ k64_swz(rows), :]
+    return out.transpose(0, 2, 1, 3, 4).reshape(RB * 16, K)[:R]

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime first, so the library bin
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpqint8.so")
 
 PQ_OK, PQ_EINVAL, PQ_ESHAPE, PQ_EALIGN, PQ_EDTYPE, PQ_ELAUNCH = 0, -1, -2, -3, -4, -5
-PQ_BF16, PQ_F16 = 0, 1
+PQ_BF16, PQ_F16, PQ_I32 = 0, 1, 2
 ABI_VERSION = 1
 
 # every entry point declared in include/pyraquant_amd.h
@@ -27,6 +27,9 @@ EXPORTS = (
     "pq_lowrank_down",
     "pq_int8_gemm",
     "pq_int8_gemm_i32",
+    "pq_int8_gemm_packed",
+    "pq_pack_k64",
+    "pq_quant_rows_packed",
     "pq_dequant_epilogue",
 )
 
@@ -43,6 +46,10 @@ _SIGNATURES = {
     "pq_int8_gemm": ([_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p,
                       _i64, _i64, _i64, _p], ctypes.c_int),
     "pq_int8_gemm_i32": ([_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
+    "pq_int8_gemm_packed": ([_p, _p, _p, _p, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p, _i64, _i64, _i64, _p],
+                            ctypes.c_int),
+    "pq_pack_k64": ([_p, _i64, _i64, _i64, _p, _p], ctypes.c_int),
+    "pq_quant_rows_packed": ([_p, _i32, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
     "pq_dequant_epilogue": ([_p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p], ctypes.c_int),
 }
 

@@ -24,6 +24,18 @@ typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
+// ---- packed K64 layout -----------------------------------------------------------------------------------------
+// Slot of 16-byte chunk c of row r' (0..15) of a 1 KB block is c ^ k64_swz(r'): among 8 consecutive rows the
+// (row parity, slot) pairs of one chunk are distinct, and among 16 consecutive rows the (row % 4, slot) pairs are,
+// so the GEMM's ds_read_b128 of consecutive rows are bank-conflict free in 128- and 256-byte bank windows.
+__host__ __device__ __forceinline__ int k64_swz(int r) { return ((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1); }
+
+// Byte offset of element (m, k) of an int8 matrix in the packed K64 layout with KT = K / 64 stages.
+__device__ __forceinline__ int64_t k64_offset(int64_t m, int k, int KT) {
+  const int r = (int)(m & 15);
+  return ((m >> 4) * KT + (k >> 6)) * 1024 + r * 64 + ((((k >> 4) & 3) ^ k64_swz(r)) << 4) + (k & 15);
+}
+
 // ---- 16-bit float <-> fp32 (exact widening; round-to-nearest-even narrowing) ----------------------------
 template <int DT>
 __device__ __forceinline__ float lo16_to_f32(uint32_t w) {
@@ -59,10 +71,19 @@ __device__ __forceinline__ uint32_t f32_to_16_bits(float f) {
   }
 }
 
-// Two fp32 values -> one dword holding two 16-bit values (lo = a, hi = b).
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> one dword holding two 16-bit values (lo = a, hi = b), round to nearest even
+// (gfx950: one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 per pair).
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return f32_to_16_bits<DT>(a) | (f32_to_16_bits<DT>(b) << 16);
+  if constexpr (DT == PQ_BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{a, b}, v2bf));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{a, b}, v2h));
+  }
 }
 
 }  // namespace pq

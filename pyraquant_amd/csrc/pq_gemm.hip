@@ -12,13 +12,13 @@
 // Per-channel / int32 kernel (gemm_dma_kernel). 256 threads = 2 x 2 wavefronts, one wavefront per SIMD.
 // A workgroup owns a BN x BM (n x m) block, each wave a (BN/2) x (BM/2) quarter held as TI x TJ
 // v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in AGPRs; 256 of them for the 256 x 256 block).
-// K advances in stages of 128 bytes through a two-stage LDS ring filled by LDS-DMA buffer loads
-// (buffer_load_dwordx4 ... lds): no VGPR staging and no ds_write. One DMA instruction fills 1 KB = 8 LDS rows
-// of 128 bytes; each lane fetches the 16-byte chunk that the XOR swizzle places at its LDS slot, so the
-// MFMA operand reads (ds_read_b128, one tile row per lane) are bank-conflict free. Within a stage the four
-// 32-byte K substeps are software-pipelined: the fragments of substep s+1 are read from LDS while the MFMAs
-// of substep s run, and the DMA of stage k+2 is interleaved with the MFMAs of the last substep of stage k.
-// One workgroup barrier per stage.
+// K advances in stages of 64 bytes through a ring of NS LDS stages (5 x 32 KB for 256 x 256 blocks) filled by
+// LDS-DMA buffer loads (buffer_load_dwordx4 ... lds): no VGPR staging, no ds_write, and NS - 1 stages of
+// prefetch in flight to cover L2 / MALL latency. One DMA instruction fills 1 KB = 16 LDS rows of 64 bytes;
+// each lane fetches the 16-byte chunk that the XOR swizzle places at its LDS slot, so the MFMA operand reads
+// (ds_read_b128, one tile row per lane) are bank-conflict free. The two 32-byte K substeps of a stage are
+// software-pipelined: the fragments of the next substep are read from LDS while the MFMAs of the current one
+// run, and the DMA of a new stage is interleaved with the MFMAs. One workgroup barrier per stage.
 //
 // Group-32 kernel (gemm_reg_kernel). Every 32-wide K group is one MFMA whose int32 partial the VALU scales
 // by s_w[g, n] into an fp32 accumulator (VGPRs); K advances in 64-byte stages through a register-staged
@@ -82,105 +82,209 @@ __device__ __forceinline__ v16f lr_mfma(v4i a, v4i b, v16f c) {
 // ---- epilogue shared by both kernels ----------------------------------------------------------------------
 // The wave's accumulators cover weight rows nbase + 32 i + [0, 32) and activation rows mbase + 32 j + [0, 32).
 // Lane holds, for tile (i, j) and register r: m = mbase + 32 j + lane % 32,
-// n = nbase + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4. Weight tile outer (its scales / bias / low-rank rows
-// loaded once), rows inner. The fp32 operations run in the reference's order (deploy/int8_exec.py:303-309).
-template <int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT, typename AccT>
-__device__ __forceinline__ void epilogue(const GemmArgs& p, AccT (&acc)[TI][TJ], int nbase, int mbase, int lane) {
-  const int rsub = lane & 31;
-  const int khalf = lane >> 5;
-#pragma unroll
-  for (int i = 0; i < TI; ++i) {
-    const int ntile = nbase + i * 32;
-    if (ntile >= p.N) continue;   // N % 32 == 0: a weight tile is entirely in or out of range
-    const int nb = ntile + 4 * khalf;
-    v4f sc[4], bi[4];
-    v4i lb[HAS_LR ? 4 : 1];
-    if constexpr (MODE != kModeI32) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        sc[q] = MODE == kModeChannel ? *reinterpret_cast<const v4f*>(p.s_w + nb + 8 * q) : v4f{};
-        bi[q] = p.bias ? *reinterpret_cast<const v4f*>(p.bias + nb + 8 * q) : v4f{};
-      }
-      if constexpr (HAS_LR) {
-        const uint16_t* lrow = p.l2t + (int64_t)(ntile + rsub) * p.R + khalf * 8;
-#pragma unroll
-        for (int rs = 0; rs < 4; ++rs) lb[rs] = rs * 16 < p.R ? *reinterpret_cast<const v4i*>(lrow + rs * 16) : v4i{};
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-      const int m = mbase + j * 32 + rsub;
-      const int mc = min(m, p.M - 1);
-      const bool mvalid = m < p.M;
-      if constexpr (MODE == kModeI32) {
-        if (mvalid) {
-          int32_t* crow = static_cast<int32_t*>(p.c) + (int64_t)m * p.ldc;
-          const v16i& v = acc[i][j];
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<v4i*>(crow + nb + 8 * q) = v4i{v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
-        }
-      } else {
-        const float sr = p.s_row[mc];
-        float y[16];
-        if constexpr (MODE == kModeChannel) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) y[r] = (float)acc[i][j][r] * (sr * sc[r >> 2][r & 3]);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) y[r] = acc[i][j][r] * sr;
-        }
-        if constexpr (HAS_LR) {
-          const uint16_t* trow = p.t + (int64_t)mc * p.ldt + khalf * 8;
-          v16f lr = v16f{};
-#pragma unroll
-          for (int rs = 0; rs < 4; ++rs) {
-            if (rs * 16 < p.R) lr = lr_mfma<LRDT>(lb[rs], *reinterpret_cast<const v4i*>(trow + rs * 16), lr);
-          }
-#pragma unroll
-          for (int r = 0; r < 16; ++r) y[r] = y[r] + lr[r];
-        }
-        if (p.bias) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) y[r] = y[r] + bi[r >> 2][r & 3];
-        }
-        if (mvalid) {
-          const int64_t orow = p.out_row_idx ? (int64_t)p.out_row_idx[m] : (int64_t)m;
-          uint16_t* crow = static_cast<uint16_t*>(p.c) + orow * p.ldc;
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<v2u*>(crow + nb + 8 * q) =
-                v2u{pack2<ODT>(y[4 * q + 0], y[4 * q + 1]), pack2<ODT>(y[4 * q + 2], y[4 * q + 3])};
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);   // keep one tile's epilogue live at a time (no AGPR mass copy)
-    }
-  }
+// n = nbase + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4. The fp32 operations run in the reference's order
+// (deploy/int8_exec.py:303-309). Operands are fetched ahead of use so that no tile waits on its own global load:
+// the per-row operands (s_row, the scatter row, the low-rank row t[m, :]) are issued by prefetch_rows() while the
+// last MFMAs run, and the per-column operands (s_w, bias, low-rank rows l2t[n, :]) of weight tile i + 1 are
+// issued before the tiles of weight tile i are computed. LRS = number of 16-wide low-rank slices held (0: none).
+// One int32 accumulator element read from its AGPR where it is used. Reading element by element keeps the
+// register allocator from copying every accumulator tile into VGPRs at once when the main loop ends (256
+// accumulators per lane do not fit next to the epilogue's operands and would spill).
+__device__ __forceinline__ int acc_read(int a) {
+  int v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
 }
 
-// ---- per-channel / int32 kernel: LDS-DMA two-stage ring, 128-byte K stages ----------------------------------
-constexpr int kBKd = 128;   // K bytes per stage
+template <int TI, int TJ, int MODE, int LRS, int LRDT, int ODT>
+struct Epilogue {
+  static constexpr bool HAS_LR = LRS > 0;
+  static constexpr int RS = HAS_LR ? LRS : 1;   // 16-wide slices of the low rank: R == 16 * LRS exactly
+  float sr[TJ];
+  int orow[TJ];
+  v4i tv[TJ][RS];
+  v4f sc[2][4], bi[2][4];
+  v4i lb[2][RS];
 
-// LDS row r (128 bytes, one tile row) stores its 16-byte chunk c at slot c ^ swz(r). Eight consecutive rows put
-// one chunk into eight different slots, and sixteen consecutive rows give sixteen distinct (row parity, slot)
-// pairs, so the ds_read_b128 of 8 (or 16) lanes reading consecutive rows touch distinct banks.
-__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+  __device__ __forceinline__ void load_cols(const GemmArgs& p, int slot, int ntile, int lane) {
+    if constexpr (MODE != kModeI32) {
+      if (ntile >= p.N) return;
+      const int nb = ntile + 4 * (lane >> 5);
+      if constexpr (MODE == kModeChannel) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) sc[slot][q] = *reinterpret_cast<const v4f*>(p.s_w + nb + 8 * q);
+      }
+      if (p.bias) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bi[slot][q] = *reinterpret_cast<const v4f*>(p.bias + nb + 8 * q);
+      }
+      if constexpr (HAS_LR) {
+        const uint16_t* lrow = p.l2t + (int64_t)(ntile + (lane & 31)) * p.R + (lane >> 5) * 8;
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs) lb[slot][rs] = *reinterpret_cast<const v4i*>(lrow + rs * 16);
+      }
+    }
+  }
 
-// s_waitcnt vmcnt(0) (expcnt / lgkmcnt left at their maxima). The compiler does not count LDS-DMA loads as
+  // per-row operands (issued under the last stage's MFMAs)
+  __device__ __forceinline__ void prefetch_rows(const GemmArgs& p, int mbase, int lane) {
+    if constexpr (MODE != kModeI32) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const int m = mbase + j * 32 + (lane & 31);
+        const int mc = min(m, p.M - 1);
+        sr[j] = p.s_row[mc];
+        if constexpr (HAS_LR) {
+          const uint16_t* trow = p.t + (int64_t)mc * p.ldt + (lane >> 5) * 8;
+#pragma unroll
+          for (int rs = 0; rs < RS; ++rs) tv[j][rs] = *reinterpret_cast<const v4i*>(trow + rs * 16);
+        }
+      }
+      if (p.out_row_idx) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) orow[j] = p.out_row_idx[min(mbase + j * 32 + (lane & 31), p.M - 1)];
+      } else {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) orow[j] = mbase + j * 32 + (lane & 31);
+      }
+    }
+  }
+
+  // Rows of the wave's output sub-tile (32 TJ rows of 32 TI outputs) staged in LDS by run(): 16-bit outputs,
+  // rows padded by 16 bytes so that the column-wise fragment writes spread over the banks.
+  static constexpr int kRowBytes = 64 * TI;
+  static constexpr int kPitch = kRowBytes + 16;
+  static constexpr int kStageBytes = 32 * TJ * kPitch + 32 * TJ * 4;   // + the rows' scatter targets
+
+  // Epilogue. int32 mode: the accumulators are stored straight from the fragments. Dequant modes: each fragment is
+  // dequantized (+ low rank, + bias) and rounded in registers, written to the wave's LDS staging area in row-major
+  // order, and the wave then stores whole rows: lane l writes 16 bytes, 4 TI lanes cover a row's 64 TI bytes, so
+  // every store instruction writes complete 128-byte lines (the fragment layout alone would write 16-byte pieces
+  // of 32 rows per instruction). `stage` is this wave's kStageBytes of LDS, free once the main loop has ended.
+  template <typename AccT>
+  __device__ __forceinline__ void run(const GemmArgs& p, AccT (&acc)[TI][TJ], int nbase, int mbase, int lane,
+                                      uint8_t* stage) {
+    const int khalf = lane >> 5;
+    const bool has_bias = p.bias != nullptr;
+    if constexpr (MODE == kModeChannel) {
+      // The accumulators are read one element at a time by acc_read; the last MFMA into any of them is at least
+      // three MFMAs back, and 24 more wait states make the MFMA -> v_accvgpr_read distance explicit.
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (MODE == kModeI32) {
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        const int ntile = nbase + i * 32;
+        if (ntile >= p.N) continue;
+        const int nb = ntile + 4 * khalf;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          const int m = mbase + j * 32 + (lane & 31);
+          if (m < p.M) {
+            int32_t* crow = static_cast<int32_t*>(p.c) + (int64_t)m * p.ldc;
+            const v16i& v = acc[i][j];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<v4i*>(crow + nb + 8 * q) = v4i{v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      return;
+    } else {
+      int* srow = reinterpret_cast<int*>(stage + 32 * TJ * kPitch);
+      if (khalf == 0) {
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) srow[j * 32 + (lane & 31)] = orow[j];
+      }
+      load_cols(p, 0, nbase, lane);
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        if (i + 1 < TI) load_cols(p, (i + 1) & 1, nbase + (i + 1) * 32, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        const int c = i & 1;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          v16f y;
+          if constexpr (MODE == kModeChannel) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) y[r] = (float)acc_read(acc[i][j][r]) * (sr[j] * sc[c][r >> 2][r & 3]);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) y[r] = acc[i][j][r] * sr[j];
+          }
+          if constexpr (HAS_LR) {
+            // y += t[m, :] . l2t[n, :] (fp32 accumulation of the 16-bit operands, deploy/int8_exec.py:304-307)
+            v16f lr = v16f{};
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs) lr = lr_mfma<LRDT>(lb[c][rs], tv[j][rs], lr);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) y[r] = y[r] + lr[r];
+          }
+          if (has_bias) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) y[r] = y[r] + bi[c][r >> 2][r & 3];
+          }
+          // fragment -> staging rows: row (32 j + lane % 32), outputs 32 i + 8 q + 4 (lane / 32) .. + 3
+          uint8_t* srow_j = stage + (j * 32 + (lane & 31)) * kPitch + (i * 32 + 4 * khalf) * 2;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<v2u*>(srow_j + 16 * q) =
+                v2u{pack2<ODT>(y[4 * q + 0], y[4 * q + 1]), pack2<ODT>(y[4 * q + 2], y[4 * q + 3])};
+          __builtin_amdgcn_sched_barrier(0);   // keep one tile's epilogue live at a time
+        }
+      }
+      // staging rows -> global: instruction s stores rows 16 s / TI + lane / (4 TI), 16 bytes per lane
+      constexpr int LPR = 4 * TI;          // lanes per row
+      constexpr int RPI = 64 / LPR;        // rows per store instruction
+      const int lr_ = lane / LPR, lc = lane % LPR;
+      const int n = nbase + lc * 8;
+      const bool nvalid = n < p.N;
+#pragma unroll 4
+      for (int s0 = 0; s0 < 32 * TJ; s0 += RPI) {
+        const int row = s0 + lr_;
+        const int m = mbase + row;
+        const v4u v = *reinterpret_cast<const v4u*>(stage + row * kPitch + lc * 16);
+        if (nvalid && m < p.M) {
+          const int64_t o = p.out_row_idx ? (int64_t)srow[row] : (int64_t)m;
+          *reinterpret_cast<v4u*>(static_cast<uint16_t*>(p.c) + o * p.ldc + n) = v;
+        }
+      }
+    }
+  }
+};
+
+// ---- per-channel / int32 kernel: LDS-DMA ring of NS stages, 64-byte K stages ---------------------------------
+constexpr int kBKd = 64;   // K bytes per stage (two 32-byte MFMA substeps)
+
+// LDS row r (64 bytes, one tile row) stores its 16-byte chunk c at slot c ^ swz(r). Among 8 consecutive rows the
+// (row parity, slot) pairs of one chunk are distinct, and among 16 consecutive rows the (row % 4, slot) pairs are,
+// so the ds_read_b128 of 8 (or 16) lanes reading consecutive rows touch distinct banks in a 128-byte (or
+// 256-byte) bank window.
+__device__ __forceinline__ int swz(int r) { return k64_swz(r); }
+
+// s_waitcnt vmcnt(N) (expcnt / lgkmcnt left at their maxima). The compiler does not count LDS-DMA loads as
 // LDS writes before a barrier, so every stage hand-over waits for them explicitly.
-__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
 
-template <int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
+template <int TI, int TJ, int NS, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
   static_assert(MODE != kModeGroup32, "group-32 runs on gemm_reg_kernel");
   constexpr int BN = 64 * TI, BM = 64 * TJ;
   constexpr int WB = BN * kBKd, AB = BM * kBKd, STAGE = WB + AB;
-  constexpr int DW = BN / 32, DA = BM / 32;   // 1 KB DMA instructions per wave and stage (W, A)
+  constexpr int DW = BN / 64, DA = BM / 64;   // 1 KB DMA instructions per wave and stage (W, A)
+  constexpr int DPW = DW + DA;
   constexpr int NF = TI + TJ;                 // fragments per substep
   constexpr int kRest = TI * TJ - NF;         // MFMAs of a substep beyond the NF that carry a fragment read
-  constexpr int kVPer = kRest > 0 ? (DW + DA) / kRest : 0;   // DMA instructions per such MFMA
-  static_assert(DW % 2 == 0 && DA % 2 == 0, "DMA parity assumes an even instruction count");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+  constexpr int kVPer = kRest > 0 ? (DPW + kRest - 1) / (kRest > 0 ? kRest : 1) : 0;   // DMA per such MFMA
+  static_assert(NS >= 3 && NS * STAGE <= 160 * 1024, "LDS ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -193,40 +297,57 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
   const int m0 = tm * BM;
   const int n0 = tn * BN;
 
-  // Buffer resources based at the block's first row. Rows past M / N, and the whole DMA of a stage past the
-  // end of K (offset kOOB), are outside num_records: those loads read no memory.
+  // Buffer resources based at the block's first row. Rows past M / N, and the DMA of a stage past the end of K
+  // (offset kOOB), lie outside num_records: those loads read no memory.
+  //
+  // Row-major operands: DMA instruction i of this wave fills LDS bytes [(wave * D + i) * 1024, +1024) of its
+  // operand tile: rows (wave * D + i) * 16 + lane / 4, slot lane % 4. The chunk stored at that slot is
+  // (lane % 4) ^ swz(row), and row % 16 == lane / 4, so it depends on the lane only.
+  // Packed operands (packed K64 layout, see pq_pack_k64): the same 1 KB is the contiguous block (row block, kt)
+  // at ((row block) * KT + kt) * 1024, already swizzled: lane l copies bytes [16 l, 16 l + 16).
+  const int KT = p.K / kBKd;
   const int rows_w = min(BN, p.N - n0), rows_a = min(BM, p.M - m0);
-  const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.w + (int64_t)n0 * p.ldw), (short)0, (int)(rows_w * p.ldw), kBufferWord3);
-  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.a + (int64_t)m0 * p.lda), (short)0, (int)(rows_a * p.lda), kBufferWord3);
-
-  // DMA instruction i of this wave fills LDS bytes [(wave * D + i) * 1024, +1024) of its operand tile: rows
-  // (wave * D + i) * 8 + lane / 8, slot lane % 8. The chunk stored at that slot is
-  // (lane % 8) ^ swz(row) = (lane % 8) ^ (lane / 8) ^ (i % 2).
-  const int l8 = lane >> 3;
-  const int ce = ((lane & 7) ^ l8) << 4;
-  const int co = ((lane & 7) ^ l8 ^ 1) << 4;
-  const int vw = (wave * DW * 8 + l8) * (int)p.ldw;
-  const int va = (wave * DA * 8 + l8) * (int)p.lda;
-  const int stw = 8 * (int)p.ldw;
-  const int sta = 8 * (int)p.lda;
+  const int l4 = lane >> 2;
+  int vw, va, stw, sta;
+  __amdgpu_buffer_rsrc_t rs_w, rs_a;
+  if constexpr (PACKED) {
+    const int blk_w = (rows_w + 15) / 16, blk_a = (rows_a + 15) / 16;
+    rs_w = __builtin_amdgcn_make_buffer_rsrc((void*)(p.w + (int64_t)(n0 / 16) * KT * 1024), (short)0,
+                                             blk_w * KT * 1024, kBufferWord3);
+    rs_a = __builtin_amdgcn_make_buffer_rsrc((void*)(p.a + (int64_t)(m0 / 16) * KT * 1024), (short)0,
+                                             blk_a * KT * 1024, kBufferWord3);
+    vw = wave * DW * KT * 1024 + lane * 16;
+    va = wave * DA * KT * 1024 + lane * 16;
+    stw = KT * 1024;
+    sta = KT * 1024;
+  } else {
+    rs_w = __builtin_amdgcn_make_buffer_rsrc((void*)(p.w + (int64_t)n0 * p.ldw), (short)0, (int)(rows_w * p.ldw),
+                                             kBufferWord3);
+    rs_a = __builtin_amdgcn_make_buffer_rsrc((void*)(p.a + (int64_t)m0 * p.lda), (short)0, (int)(rows_a * p.lda),
+                                             kBufferWord3);
+    const int cdma = ((lane & 3) ^ swz(l4)) << 4;
+    vw = (wave * DW * 16 + l4) * (int)p.ldw + cdma;
+    va = (wave * DA * 16 + l4) * (int)p.lda + cdma;
+    stw = 16 * (int)p.ldw;
+    sta = 16 * (int)p.lda;
+  }
+  constexpr int kStageStep = PACKED ? 1024 : kBKd;   // buffer offset of one K stage
 
   auto dma = [&](int buf, int koff) {
     uint8_t* sb = smem + buf * STAGE;
 #pragma unroll
     for (int i = 0; i < DW; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, (lds_void_t*)(sb + (wave * DW + i) * 1024), 16,
-                                               vw + i * stw + ((i & 1) ? co : ce) + koff, 0, 0, 0);
+                                               vw + i * stw + koff, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < DA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void_t*)(sb + WB + (wave * DA + i) * 1024), 16,
-                                               va + i * sta + ((i & 1) ? co : ce) + koff, 0, 0, 0);
+                                               va + i * sta + koff, 0, 0, 0);
   };
 
   // MFMA operand reads: lane reads tile row (lane % 32) of each 32-row fragment, K chunk 2 s + lane / 32 of
-  // substep s. Fragment rows are 32-aligned, so swz(row) depends on the lane only.
-  const int sw = (lane & 7) ^ ((lane >> 3) & 1);
+  // substep s. Fragment rows are 32-aligned, so swz(row) = swz(lane % 16).
+  const int sw = swz(lane & 15);
   const int kh = lane >> 5;
   const int fw_off = (wn * (BN / 2) + (lane & 31)) * kBKd;
   const int fa_off = WB + (wm * (BM / 2) + (lane & 31)) * kBKd;
@@ -254,9 +375,9 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
   };
 
   // Instruction order inside one substep: the NF fragment reads of the next substep are spread over the first NF
-  // MFMAs of this one. In the last substep of a stage the remaining MFMAs also carry the DMA of the stage after
-  // next (issued after the reads: the scheduler keeps LDS reads ahead of a later LDS-DMA it cannot disambiguate).
-  // sched_barrier(0) keeps each substep's MFMAs on its side of the stage barrier.
+  // MFMAs of this one. In the second substep of a stage the remaining MFMAs also carry the DMA of the stage NS
+  // ahead (issued after the reads: the scheduler keeps LDS reads ahead of a later LDS-DMA it cannot
+  // disambiguate). sched_barrier(0) keeps each substep's MFMAs on its side of the stage barrier.
   auto interleave = [&](auto with_dma) {
 #pragma unroll
     for (int q = 0; q < NF; ++q) {
@@ -266,8 +387,8 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
     if constexpr (decltype(with_dma)::value && kRest > 0) {
 #pragma unroll
       for (int q = 0; q < kRest; ++q) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);         // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x010, kVPer, 0);     // VMEM (LDS-DMA)
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x010, kVPer, 0);   // VMEM (LDS-DMA)
       }
     } else if constexpr (kRest > 0) {
       __builtin_amdgcn_sched_group_barrier(0x008, kRest, 0);
@@ -277,46 +398,41 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
   using no_dma = std::integral_constant<bool, false>;
   using with_dma = std::integral_constant<bool, true>;
 
-  const int KT = (p.K + kBKd - 1) / kBKd;
-  const bool ktail = (p.K % kBKd) != 0;   // K % 128 == 64: the last stage holds two substeps
-  dma(0, 0);
-  dma(1, KT > 1 ? kBKd : kOOB);
-  wait_dma();
+  // Ring: stage s lives in buffer s % NS. The DMA of stage s is issued after the barrier of iteration s - NS and
+  // must have landed at the barrier that ends iteration s - 1, NS - 1 iterations later; in between, the DMAs of
+  // NS - 2 younger stages may still be in flight, hence vmcnt((NS - 2) * DPW).
+#pragma unroll
+  for (int st = 0; st < NS; ++st) dma(st, st < KT ? st * kStageStep : kOOB);
+  wait_dma<(NS - 1) * DPW>();
   __syncthreads();
   rd(f0, 0, 0);
+  int b = 0;
   for (int kt = 0; kt < KT - 1; ++kt) {
-    const int b = kt & 1;
+    const int bn = b + 1 == NS ? 0 : b + 1;
     rd(f1, b, 1);
     mm(f0);
     interleave(no_dma{});
-    rd(f0, b, 2);
-    mm(f1);
-    interleave(no_dma{});
-    rd(f1, b, 3);
-    mm(f0);
-    interleave(no_dma{});
-    wait_dma();        // this wave's DMA of stage kt + 1 has landed
-    __syncthreads();   // every wave's has, and every wave is done reading buffer b
+    wait_dma<(NS - 2) * DPW>();   // this wave's DMA of stage kt + 1 has landed
+    __syncthreads();              // every wave's has, and every wave is done reading buffer b
     __builtin_amdgcn_sched_barrier(0);
-    rd(f0, b ^ 1, 0);
-    dma(b, kt + 2 < KT ? (kt + 2) * kBKd : kOOB);
+    rd(f0, bn, 0);
+    dma(b, kt + NS < KT ? (kt + NS) * kStageStep : kOOB);
     mm(f1);
     interleave(with_dma{});
+    b = bn;
   }
-  {
-    const int b = (KT - 1) & 1;
-    rd(f1, b, 1);
-    mm(f0);
-    if (!ktail) {
-      rd(f0, b, 2);
-      mm(f1);
-      rd(f1, b, 3);
-      mm(f0);
-    }
-    mm(f1);
-  }
-
-  epilogue<TI, TJ, MODE, HAS_LR, LRDT, ODT>(p, acc, n0 + wn * (BN / 2), m0 + wm * (BM / 2), lane);
+  // last stage: the epilogue's operands are fetched under its MFMAs
+  Epilogue<TI, TJ, MODE, LRS, LRDT, ODT> epi;
+  const int nbase = n0 + wn * (BN / 2), mbase = m0 + wm * (BM / 2);
+  epi.prefetch_rows(p, mbase, lane);
+  rd(f1, b, 1);
+  mm(f0);
+  mm(f1);
+  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT>;
+  static_assert(4 * Epi::kStageBytes <= NS * STAGE, "output staging must fit the LDS ring");
+  wait_dma<0>();     // the out-of-range DMAs of the last iterations may still target the ring
+  __syncthreads();   // every wave is done reading the ring: it becomes the output staging area
+  epi.run(p, acc, nbase, mbase, lane, smem + wave * Epi::kStageBytes);
 }
 
 // ---- group-32 kernel: register-staged LDS double buffer, 64-byte K stages ------------------------------------
@@ -325,7 +441,7 @@ constexpr int kBK = 64;   // K bytes per stage
 // Byte offset of 16-byte chunk `chunk` of LDS row `row` (rows of 64 bytes, swizzled with row bits 1..2).
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 3)) << 4); }
 
-template <int WN, int WM, int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
+template <int WN, int WM, int TI, int TJ, int MODE, int LRS, int LRDT, int ODT>
 __global__ __attribute__((amdgpu_flat_work_group_size(WN * WM * 64, WN * WM * 64)))
 void gemm_reg_kernel(const GemmArgs p) {
   constexpr int NT = WN * WM * 64;
@@ -336,7 +452,11 @@ void gemm_reg_kernel(const GemmArgs p) {
   static_assert(CW * NT * 16 == BN * kBK && CA * NT * 16 == BM * kBK, "tile / thread mismatch");
   constexpr int ROWS_PER_PASS = NT / 4;    // 4 chunks per 64-byte row
 
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][(BN + BM) * kBK];
+  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT>;
+  constexpr int kRing = (BN + BM) * kBK;                                        // one stage of the double buffer
+  constexpr int kSmem = 2 * kRing > WN * WM * Epi::kStageBytes ? 2 * kRing : WN * WM * Epi::kStageBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t smem_raw[kSmem];
+  uint8_t(*smem)[kRing] = reinterpret_cast<uint8_t(*)[kRing]>(smem_raw);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -455,7 +575,10 @@ void gemm_reg_kernel(const GemmArgs p) {
     __syncthreads();
   }
 
-  epilogue<TI, TJ, MODE, HAS_LR, LRDT, ODT>(p, acc, n0 + wn * TI * 32, m0 + wm * TJ * 32, lane);
+  Epi epi;
+  epi.prefetch_rows(p, m0 + wm * TJ * 32, lane);
+  __syncthreads();   // the LDS double buffer becomes the output staging area
+  epi.run(p, acc, n0 + wn * TI * 32, m0 + wm * TJ * 32, lane, smem_raw + wave * Epi::kStageBytes);
 }
 
 // ---- launchers ---------------------------------------------------------------------------------------------
@@ -468,21 +591,23 @@ int grid_of(GemmArgs& a, int BM, int BN, dim3& grid) {
   return PQ_OK;
 }
 
-template <int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
+template <int TI, int TJ, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 int launch_dma(GemmArgs& a, hipStream_t stream) {
+  // as many 64-byte K stages as fit the 160 KB LDS: 5 x 32 KB for 256 x 256 blocks, 8 x 16 KB for 128 x 128
+  constexpr int NS = TI * TJ >= 16 ? 5 : 8;
   dim3 grid;
   const int st = grid_of(a, 64 * TJ, 64 * TI, grid);
   if (st != PQ_OK) return st;
-  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, MODE, HAS_LR, LRDT, ODT>), grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, NS, PACKED, MODE, LRS, LRDT, ODT>), grid, dim3(256), 0, stream, a);
   return check_launch("int8_gemm");
 }
 
-template <int WN, int WM, int TI, int TJ, int MODE, bool HAS_LR, int LRDT, int ODT>
+template <int WN, int WM, int TI, int TJ, int MODE, int LRS, int LRDT, int ODT>
 int launch_reg(GemmArgs& a, hipStream_t stream) {
   dim3 grid;
   const int st = grid_of(a, WM * TJ * 32, WN * TI * 32, grid);
   if (st != PQ_OK) return st;
-  hipLaunchKernelGGL((gemm_reg_kernel<WN, WM, TI, TJ, MODE, HAS_LR, LRDT, ODT>), grid, dim3(WN * WM * 64), 0,
+  hipLaunchKernelGGL((gemm_reg_kernel<WN, WM, TI, TJ, MODE, LRS, LRDT, ODT>), grid, dim3(WN * WM * 64), 0,
                      stream, a);
   return check_launch("int8_gemm");
 }
@@ -493,29 +618,40 @@ inline bool big_tiles(const GemmArgs& a) {
   return t256 >= 512;
 }
 
-template <int MODE, bool HAS_LR, int LRDT, int ODT>
+template <bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
   if constexpr (MODE == kModeGroup32) {
     // fp32 accumulators live in VGPRs (the VALU rescales them every group): 2 x 2 waves of 64 x 64
-    return launch_reg<2, 2, 2, 2, MODE, HAS_LR, LRDT, ODT>(a, stream);
+    static_assert(!PACKED, "group-32 takes row-major operands");
+    return launch_reg<2, 2, 2, 2, MODE, LRS, LRDT, ODT>(a, stream);
   } else {
-    if (big_tiles(a)) return launch_dma<4, 4, MODE, HAS_LR, LRDT, ODT>(a, stream);
-    return launch_dma<2, 2, MODE, HAS_LR, LRDT, ODT>(a, stream);
+    if (big_tiles(a)) return launch_dma<4, 4, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    return launch_dma<2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
   }
 }
 
-template <int MODE>
+// low-rank slices held in registers: exactly R / 16 (R = 16, 32 or 64)
+template <bool PACKED, int MODE, int DT>
+int dispatch_rank(GemmArgs& a, hipStream_t stream) {
+  if (a.R == 32) return dispatch_tiles<PACKED, MODE, 2, DT, DT>(a, stream);
+  if (a.R == 16) return dispatch_tiles<PACKED, MODE, 1, DT, DT>(a, stream);
+  return dispatch_tiles<PACKED, MODE, 4, DT, DT>(a, stream);
+}
+
+// The low-rank operands t / l2t share the output's 16-bit type (the reference computes t in lr_A's dtype and
+// Int8Linear keeps lr_A in the model dtype, deploy/int8_exec.py:371-390).
+template <bool PACKED, int MODE>
 int dispatch_dtypes(GemmArgs& a, bool has_lr, int lr_dtype, int out_dtype, hipStream_t stream) {
+  if (has_lr && lr_dtype != out_dtype)
+    return set_error(PQ_EDTYPE, "pq_int8_gemm: low-rank dtype %d must equal the output dtype %d", lr_dtype, out_dtype);
   if (out_dtype == PQ_BF16) {
-    if (!has_lr) return dispatch_tiles<MODE, false, PQ_BF16, PQ_BF16>(a, stream);
-    if (lr_dtype == PQ_BF16) return dispatch_tiles<MODE, true, PQ_BF16, PQ_BF16>(a, stream);
-    if (lr_dtype == PQ_F16) return dispatch_tiles<MODE, true, PQ_F16, PQ_BF16>(a, stream);
+    if (!has_lr) return dispatch_tiles<PACKED, MODE, 0, PQ_BF16, PQ_BF16>(a, stream);
+    return dispatch_rank<PACKED, MODE, PQ_BF16>(a, stream);
   } else if (out_dtype == PQ_F16) {
-    if (!has_lr) return dispatch_tiles<MODE, false, PQ_F16, PQ_F16>(a, stream);
-    if (lr_dtype == PQ_BF16) return dispatch_tiles<MODE, true, PQ_BF16, PQ_F16>(a, stream);
-    if (lr_dtype == PQ_F16) return dispatch_tiles<MODE, true, PQ_F16, PQ_F16>(a, stream);
+    if (!has_lr) return dispatch_tiles<PACKED, MODE, 0, PQ_F16, PQ_F16>(a, stream);
+    return dispatch_rank<PACKED, MODE, PQ_F16>(a, stream);
   }
-  return set_error(PQ_EDTYPE, "pq_int8_gemm: unsupported dtype (out %d, low-rank %d)", out_dtype, lr_dtype);
+  return set_error(PQ_EDTYPE, "pq_int8_gemm: unsupported output dtype %d", out_dtype);
 }
 
 int check_common(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
@@ -555,8 +691,8 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
   const bool has_lr = (t != nullptr) || (l2t != nullptr);
   if (has_lr) {
     if (!t || !l2t) return set_error(PQ_EINVAL, "pq_int8_gemm: low-rank needs both t and l2t");
-    if (R < 16 || R > 64 || R % 16 != 0)
-      return set_error(PQ_ESHAPE, "pq_int8_gemm: low-rank rank R=%lld must be 16, 32, 48 or 64", (long long)R);
+    if (R != 16 && R != 32 && R != 64)
+      return set_error(PQ_ESHAPE, "pq_int8_gemm: low-rank rank R=%lld must be 16, 32 or 64", (long long)R);
     if (ldt < R || ldt % 8 != 0 || (uintptr_t)t % 16 || (uintptr_t)l2t % 16)
       return set_error(PQ_EALIGN, "pq_int8_gemm: t, l2t must be 16-byte aligned with ldt %% 8 == 0");
   }
@@ -566,8 +702,8 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
   args.c = c; args.out_row_idx = out_row_idx;
   args.lda = lda; args.ldw = ldw; args.ldt = ldt; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K; args.R = (int)R;
-  if (group == 32) return dispatch_dtypes<kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
-  return dispatch_dtypes<kModeChannel>(args, has_lr, lr_dtype, out_dtype, stream);
+  if (group == 32) return dispatch_dtypes<false, kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
+  return dispatch_dtypes<false, kModeChannel>(args, has_lr, lr_dtype, out_dtype, stream);
 }
 
 extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int32_t* c,
@@ -582,6 +718,50 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
   args.a = a; args.w = w; args.c = c;
   args.lda = lda; args.ldw = ldw; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
-  if (big_tiles(args)) return launch_dma<4, 4, kModeI32, false, PQ_BF16, PQ_BF16>(args, stream);
-  return launch_dma<2, 2, kModeI32, false, PQ_BF16, PQ_BF16>(args, stream);
+  if (big_tiles(args)) return launch_dma<4, 4, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+  return launch_dma<2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+}
+
+extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
+                                   const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R,
+                                   int32_t lr_dtype, void* c, int64_t ldc, int32_t out_dtype,
+                                   const int32_t* out_row_idx, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  if (M < 0 || N < 1 || K < 1) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: bad shape");
+  if (K % 64 != 0 || N % 64 != 0)
+    return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: need K %% 64 == 0 and N %% 64 == 0 (K=%lld, N=%lld)",
+                     (long long)K, (long long)N);
+  // packed offsets of one 256-row tile (16 blocks of K / 64 KB) must stay below kOOB
+  if (M > 0x7fffffffLL - 512 || N > (1 << 30) || 16 * (K / 64) * 1024 + 1024 > kOOB)
+    return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: shape too large");
+  if (M == 0) return PQ_OK;
+  if (!ap || !wp || !c) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null operand");
+  if ((uintptr_t)ap % 16 || (uintptr_t)wp % 16) return set_error(PQ_EALIGN, "pq_int8_gemm_packed: ap / wp must be 16-byte aligned");
+  GemmArgs args{};
+  args.a = ap; args.w = wp; args.c = c;
+  args.M = (int)M; args.N = (int)N; args.K = (int)K;
+  if (out_dtype == PQ_I32) {
+    if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 16)
+      return set_error(PQ_EALIGN, "pq_int8_gemm_packed: int32 c must be 16-byte aligned with ldc %% 4 == 0");
+    args.ldc = ldc;
+    if (big_tiles(args)) return launch_dma<4, 4, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+    return launch_dma<2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+  }
+  if (!s_row || !s_w) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null s_row / s_w");
+  if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 8)
+    return set_error(PQ_EALIGN, "pq_int8_gemm_packed: c must be 8-byte aligned with ldc >= N, ldc %% 4 == 0");
+  if ((uintptr_t)s_w % 16 || (bias && (uintptr_t)bias % 16))
+    return set_error(PQ_EALIGN, "pq_int8_gemm_packed: s_w and bias must be 16-byte aligned");
+  const bool has_lr = (t != nullptr) || (l2t != nullptr);
+  if (has_lr) {
+    if (!t || !l2t) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: low-rank needs both t and l2t");
+    if (R != 16 && R != 32 && R != 64)
+      return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: low-rank rank R=%lld must be 16, 32 or 64", (long long)R);
+    if (ldt < R || ldt % 8 != 0 || (uintptr_t)t % 16 || (uintptr_t)l2t % 16)
+      return set_error(PQ_EALIGN, "pq_int8_gemm_packed: t, l2t must be 16-byte aligned with ldt %% 8 == 0");
+  }
+  args.s_row = s_row; args.s_w = s_w; args.bias = bias;
+  args.t = static_cast<const uint16_t*>(t); args.l2t = static_cast<const uint16_t*>(l2t);
+  args.out_row_idx = out_row_idx;
+  args.ldt = ldt; args.ldc = ldc; args.R = (int)R;
+  return dispatch_dtypes<true, kModeChannel>(args, has_lr, lr_dtype, out_dtype, stream);
 }

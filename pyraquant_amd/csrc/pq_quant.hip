@@ -82,16 +82,27 @@ __device__ __forceinline__ float absmax_from_bits(uint32_t mag16) {
 }
 
 // Vectorised quantizer: one wave per row, CH 16-byte chunks per lane, 4 rows per 256-thread block.
-template <int DT, int CH>
+// PACKED: codes go to the packed K64 layout (8-byte stores at k64_offset), and the waves of the padding rows
+// M .. 16 * ceil(M / 16) - 1 write zeros there.
+template <int DT, int CH, bool PACKED>
 __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
     int8_t* __restrict__ q, float* __restrict__ s) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int nvec = K >> 3;
+  if constexpr (PACKED) {
+    if (m >= M) {
+      if (m < ((M + 15) & ~15LL)) {
+        for (int idx = lane; idx < nvec; idx += 64)
+          *reinterpret_cast<v2u*>(q + k64_offset(m, idx * 8, K >> 6)) = v2u{0u, 0u};
+      }
+      return;
+    }
+  }
   if (m >= M) return;
   const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
   const v4u* __restrict__ xr = reinterpret_cast<const v4u*>(x + src * ldx);
-  const int nvec = K >> 3;
   v4u v[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
@@ -115,18 +126,33 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int idx = c * 64 + lane;
-    if (idx < nvec) qr[idx] = quant_chunk<DT>(v[c], sc, rc);
+    if (idx < nvec) {
+      const v2u codes = quant_chunk<DT>(v[c], sc, rc);
+      if constexpr (PACKED) {
+        *reinterpret_cast<v2u*>(q + k64_offset(m, idx * 8, K >> 6)) = codes;
+      } else {
+        qr[idx] = codes;
+      }
+    }
   }
   if (lane == 0) s[m] = sc;
 }
 
 // Per-element quantizer for unaligned rows or odd K: one wave per row, two sweeps over the row.
-template <int DT>
+template <int DT, bool PACKED>
 __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
     int8_t* __restrict__ q, float* __restrict__ s) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if constexpr (PACKED) {
+    if (m >= M) {
+      if (m < ((M + 15) & ~15LL)) {
+        for (int k = lane; k < K; k += 64) q[k64_offset(m, k, K >> 6)] = 0;
+      }
+      return;
+    }
+  }
   if (m >= M) return;
   const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
   const uint16_t* __restrict__ xr = x + src * ldx;
@@ -141,23 +167,29 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
   int8_t* __restrict__ qr = q + m * (int64_t)K;
   for (int k = lane; k < K; k += 64) {
     const float f = lo16_to_f32<DT>(xr[k]);
-    qr[k] = (int8_t)(__float_as_uint(code_exact(f, sc)) & 0xffu);
+    const int8_t code = (int8_t)(__float_as_uint(code_exact(f, sc)) & 0xffu);
+    if constexpr (PACKED) {
+      q[k64_offset(m, k, K >> 6)] = code;
+    } else {
+      qr[k] = code;
+    }
   }
   if (lane == 0) s[m] = sc;
 }
 
-template <int DT>
+template <int DT, bool PACKED>
 int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t* row_idx, int8_t* q,
                  float* s, hipStream_t stream) {
   const dim3 block(256);
-  const dim3 grid((unsigned)((M + 3) / 4));
+  const int64_t rows = PACKED ? ((M + 15) & ~15LL) : M;
+  const dim3 grid((unsigned)((rows + 3) / 4));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const bool vec = ((uintptr_t)x % 16 == 0) && (ldx % 8 == 0) && (K % 8 == 0) && ((uintptr_t)q % 8 == 0);
   const int need = (int)((K / 8 + 63) / 64);
   if (vec && need <= 32) {
 #define PQ_QCASE(C)                                                                                       \
   if (need <= C) {                                                                                        \
-    hipLaunchKernelGGL((quant_rows_vec_kernel<DT, C>), grid, block, 0, stream, xp, ldx, (int)K, M,        \
+    hipLaunchKernelGGL((quant_rows_vec_kernel<DT, C, PACKED>), grid, block, 0, stream, xp, ldx, (int)K, M, \
                        row_idx, q, s);                                                                    \
     return check_launch("quant_rows_vec");                                                                \
   }
@@ -165,7 +197,7 @@ int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t
     PQ_QCASE(12) PQ_QCASE(16) PQ_QCASE(20) PQ_QCASE(24) PQ_QCASE(32)
 #undef PQ_QCASE
   }
-  hipLaunchKernelGGL((quant_rows_scalar_kernel<DT>), grid, block, 0, stream, xp, ldx, (int)K, M, row_idx,
+  hipLaunchKernelGGL((quant_rows_scalar_kernel<DT, PACKED>), grid, block, 0, stream, xp, ldx, (int)K, M, row_idx,
                      q, s);
   return check_launch("quant_rows_scalar");
 }
@@ -240,6 +272,24 @@ __global__ __launch_bounds__(256) void quant_weight_kernel(const float* __restri
   if (lane == 0) s[seg] = sc;
 }
 
+// ---- row-major int8 -> packed K64 layout (one-off, weights) --------------------------------------------------
+// One thread per 16-byte slot of the destination: slot (r', p) of block (rb, kt) receives chunk p ^ swz(r') of
+// row 16 rb + r' (zeros past the last row).
+__global__ __launch_bounds__(256) void pack_k64_kernel(const int8_t* __restrict__ src, int64_t R, int KT, int64_t lds,
+                                                       int8_t* __restrict__ dst, int64_t nslots) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= nslots) return;
+  const int64_t blk = t >> 6;
+  const int within = (int)(t & 63);
+  const int rr = within >> 2, slot = within & 3;
+  const int64_t rb = blk / KT;
+  const int kt = (int)(blk - rb * KT);
+  const int64_t r = rb * 16 + rr;
+  v4i v = {0, 0, 0, 0};
+  if (r < R) v = *reinterpret_cast<const v4i*>(src + r * lds + kt * 64 + ((slot ^ k64_swz(rr)) << 4));
+  *reinterpret_cast<v4i*>(dst + t * 16) = v;
+}
+
 // ---- dequant epilogue over a materialised int32 accumulator ----------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(256) void dequant_epilogue_kernel(
@@ -298,9 +348,23 @@ extern "C" int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t 
   if (!x || !q || !s) return set_error(PQ_EINVAL, "pq_quant_rows: null pointer");
   if (ldx < K) return set_error(PQ_ESHAPE, "pq_quant_rows: ldx=%lld < K=%lld", (long long)ldx, (long long)K);
   if (K > (1LL << 30) || M > (1LL << 40)) return set_error(PQ_ESHAPE, "pq_quant_rows: shape too large");
-  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16>(x, M, K, ldx, row_idx, q, s, stream);
-  if (x_dtype == PQ_F16) return launch_quant<PQ_F16>(x, M, K, ldx, row_idx, q, s, stream);
+  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, false>(x, M, K, ldx, row_idx, q, s, stream);
+  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, false>(x, M, K, ldx, row_idx, q, s, stream);
   return set_error(PQ_EDTYPE, "pq_quant_rows: unsupported dtype code %d", (int)x_dtype);
+}
+
+extern "C" int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+                                    const int32_t* row_idx, int8_t* qp, float* s, hipStream_t stream) {
+  if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+  if (K % 64 != 0) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: K=%lld must be a multiple of 64", (long long)K);
+  if (M == 0) return PQ_OK;
+  if (!x || !qp || !s) return set_error(PQ_EINVAL, "pq_quant_rows_packed: null pointer");
+  if ((uintptr_t)qp % 16) return set_error(PQ_EALIGN, "pq_quant_rows_packed: qp must be 16-byte aligned");
+  if (ldx < K) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: ldx=%lld < K=%lld", (long long)ldx, (long long)K);
+  if (K > (1LL << 30) || M > (1LL << 40)) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: shape too large");
+  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, true>(x, M, K, ldx, row_idx, qp, s, stream);
+  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, true>(x, M, K, ldx, row_idx, qp, s, stream);
+  return set_error(PQ_EDTYPE, "pq_quant_rows_packed: unsupported dtype code %d", (int)x_dtype);
 }
 
 extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t ldx,
@@ -370,4 +434,16 @@ extern "C" int pq_quant_weight(const float* w, int64_t N, int64_t K, int64_t ldw
   hipLaunchKernelGGL(quant_weight_kernel, dim3((unsigned)((segs + 3) / 4)), dim3(256), 0, stream, w, ldw, (int)N,
                      (int)K, g, q, s);
   return check_launch("quant_weight");
+}
+
+extern "C" int pq_pack_k64(const int8_t* src, int64_t R, int64_t K, int64_t lds, int8_t* dst, hipStream_t stream) {
+  if (R < 0 || K < 1 || K % 64 != 0) return set_error(PQ_ESHAPE, "pq_pack_k64: need R >= 0 and K %% 64 == 0 (K=%lld)", (long long)K);
+  if (R == 0) return PQ_OK;
+  if (!src || !dst) return set_error(PQ_EINVAL, "pq_pack_k64: null pointer");
+  if (lds < K || lds % 16 || (uintptr_t)src % 16 || (uintptr_t)dst % 16)
+    return set_error(PQ_EALIGN, "pq_pack_k64: src / dst 16-byte aligned, lds %% 16 == 0 and lds >= K required");
+  const int64_t nslots = ((R + 15) / 16) * (K / 64) * 64;
+  hipLaunchKernelGGL(pack_k64_kernel, dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, stream, src, R,
+                     (int)(K / 64), lds, dst, nslots);
+  return check_launch("pack_k64");
 }

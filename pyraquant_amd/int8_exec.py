@@ -12,8 +12,9 @@ Drop-in surface (same names, argument meaning and error types as deploy/int8_exe
   is_bf16_whitelisted, convert_linears_to_int8, warm_kernels                 (:415-474)
   FLUX_TOKEN_SHAPES, _bench, selftest_and_bench, CLI                         (:478-588)
 Additions for the MI355X build: the routed row gather (``row_idx``) and scatter (``out_row_idx``),
-group-32 weight scales (``group_size=32``), the HIP low-rank down-projection ``lowrank_down`` and the
-int32 accumulator entry ``int8_gemm_i32``.
+group-32 weight scales (``group_size=32``), the HIP low-rank down-projection ``lowrank_down``, the
+int32 accumulator entry ``int8_gemm_i32``, and the packed K64 layer path (``pack_k64``, ``quant_rows_packed``,
+``int8_gemm_packed``) that Int8Linear.forward runs on.
 
 There is one backend, "hip" (the reference's fused "triton" path; the name "triton" is accepted as an alias
 so existing ``--int8-backend triton`` flags keep working). The reference's "cublas" path (an int32 round
@@ -191,6 +192,83 @@ def int8_gemm_i32(xq: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
     return c
 
 
+# --------------------------------------------------------------------------- packed K64 layer path
+def packed_rows(rows: int) -> int:
+    """Rows of a packed K64 buffer holding `rows` rows (a multiple of 16)."""
+    return (rows + 15) // 16 * 16
+
+
+def pack_k64(w_int8: torch.Tensor) -> torch.Tensor:
+    """Row-major int8 [R, K] -> packed K64 layout (flat int8 tensor of packed_rows(R) * K bytes), pq_pack_k64.
+    Int8Linear packs its weights once at conversion."""
+    assert w_int8.dim() == 2 and w_int8.dtype == torch.int8 and w_int8.is_cuda and w_int8.stride(1) == 1
+    R, K = w_int8.shape
+    assert K % 64 == 0, K
+    out = torch.empty((packed_rows(R) * K,), dtype=torch.int8, device=w_int8.device)
+    L = _lib.load()
+    _lib.check(L.pq_pack_k64(_lib.ptr(w_int8), R, K, w_int8.stride(0), _lib.ptr(out), _lib.stream_of(w_int8.device)),
+               "pack_k64")
+    return out
+
+
+def quant_rows_packed(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """quant_rows with the codes written in the packed K64 layout (flat int8 [packed_rows(M) * K]) for
+    int8_gemm_packed; scales as quant_rows. K % 64 == 0."""
+    assert x2.dim() == 2 and x2.is_cuda
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    rows, K = x2.shape
+    ri = _row_index(row_idx, x2.device)
+    M = rows if ri is None else ri.shape[0]
+    q = torch.empty((packed_rows(M) * K,), dtype=torch.int8, device=x2.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x2.device)
+    L = _lib.load()
+    _lib.check(L.pq_quant_rows_packed(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), _lib.ptr(ri),
+                                      _lib.ptr(q), _lib.ptr(s), _lib.stream_of(x2.device)), "quant_rows_packed")
+    return q, s
+
+
+def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor, w_scale: torch.Tensor,
+                     bias: Optional[torch.Tensor], M: int, N: int, K: int, out_dtype: torch.dtype, *,
+                     t: Optional[torch.Tensor] = None, l2t: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The fused GEMM over packed K64 operands (pq_int8_gemm_packed): xq_p from quant_rows_packed, w_p from
+    pack_k64. out_dtype torch.int32 returns the raw accumulator."""
+    assert xq_p.dtype == torch.int8 and w_p.dtype == torch.int8
+    _check_cuda(xq_p, s_row, w_p, w_scale, bias, t, l2t, out, out_row_idx)
+    assert xq_p.numel() >= packed_rows(M) * K and w_p.numel() >= packed_rows(N) * K
+    ori = _row_index(out_row_idx, xq_p.device)
+    L = _lib.load()
+    if out_dtype == torch.int32:
+        c = torch.empty((M, N), dtype=torch.int32, device=xq_p.device)
+        _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), None, None, None, None, 0, None, 0, 0,
+                                         _lib.ptr(c), N, _lib.PQ_I32, None, M, N, K, _lib.stream_of(xq_p.device)),
+                   "int8_gemm_packed")
+        return c
+    assert s_row.dtype == torch.float32 and s_row.is_contiguous() and s_row.numel() >= M
+    assert w_scale.dtype == torch.float32 and w_scale.is_contiguous() and w_scale.numel() == N
+    if bias is not None:
+        assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == N
+    if ori is not None:
+        assert ori.shape[0] == M and out is not None, "a scatter needs the destination canvas (out=)"
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=xq_p.device)
+    assert out.dtype == out_dtype and out.dim() == 2 and out.shape[1] == N and out.stride(1) == 1
+    if ori is None:
+        assert out.shape[0] >= M
+    lr_code, R, ldt = 0, 0, 0
+    if t is not None:
+        assert l2t is not None and t.dtype == l2t.dtype and t.stride(1) == 1 and l2t.is_contiguous()
+        R = t.shape[1]
+        assert l2t.shape == (N, R), (tuple(l2t.shape), (N, R))
+        lr_code, ldt = _lib.dtype_code(t.dtype), t.stride(0)
+    _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), _lib.ptr(s_row), _lib.ptr(w_scale),
+                                     _lib.ptr(bias), _lib.ptr(t), ldt, _lib.ptr(l2t), R, lr_code, _lib.ptr(out),
+                                     out.stride(0), _lib.dtype_code(out_dtype), _lib.ptr(ori), M, N, K,
+                                     _lib.stream_of(xq_p.device)), "int8_gemm_packed")
+    return out
+
+
 def int8_linear_2d(x2: torch.Tensor, w_int8: torch.Tensor, w_scale: torch.Tensor,
                    bias: Optional[torch.Tensor], backend: Optional[str] = None) -> torch.Tensor:
     """x2 [M,K] bf16/fp16 -> [M,N] in x2's dtype: quantizer + fused GEMM (deploy/int8_exec.py:246-261)."""
@@ -245,6 +323,12 @@ class Int8Linear(nn.Module):
         self.group_size = int(group_size)
         self.register_buffer("weight_int8", q)
         self.register_buffer("w_scale", s)
+        N, K = q.shape
+        # per-channel layers whose shape the packed GEMM takes run on the packed K64 path
+        if not group_size and K % 64 == 0 and N % 64 == 0:
+            self.register_buffer("weight_packed", pack_k64(q))
+        else:
+            self.weight_packed = None
         if group_size:
             self.register_buffer("w_scale_gn", s.t().contiguous())
         else:
@@ -278,6 +362,14 @@ class Int8Linear(nn.Module):
     def _scale_k(self) -> torch.Tensor:
         return self.w_scale_gn if self.group_size else self.w_scale
 
+    def _lr_bt(self, dtype: torch.dtype) -> Optional[torch.Tensor]:
+        """lr_B^T [N, R] in the output dtype (the fused epilogue takes t and lr_B in the output's 16-bit type)."""
+        if self.lr_Bt is None:
+            return None
+        if self.lr_Bt.dtype != dtype:
+            return self.lr_Bt.to(dtype)
+        return self.lr_Bt
+
     def forward(self, x: torch.Tensor, row_idx: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
         """y = Linear(x) through quantizer (+ low-rank down) + fused GEMM (deploy/int8_exec.py:382-408).
@@ -290,9 +382,17 @@ class Int8Linear(nn.Module):
         if self.lr_A is not None:
             xl = x2 if x2.dtype == self.lr_A.dtype else x2.to(self.lr_A.dtype)
             t = lowrank_down(xl, self.lr_At, row_idx)
-        xq, sx = quant_rows(x2, row_idx)
-        y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, t, self.lr_Bt, x2.dtype,
-                  out, out_row_idx)
+            if t.dtype != x2.dtype:
+                t = t.to(x2.dtype)
+        if self.weight_packed is not None:
+            xq, sx = quant_rows_packed(x2, row_idx)
+            y = int8_gemm_packed(xq, sx, self.weight_packed, self.w_scale, self.bias, sx.shape[0], self.out_features,
+                                 self.in_features, x2.dtype, t=t, l2t=self._lr_bt(x2.dtype), out=out,
+                                 out_row_idx=out_row_idx)
+        else:
+            xq, sx = quant_rows(x2, row_idx)
+            y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, t,
+                      self._lr_bt(x2.dtype), x2.dtype, out, out_row_idx)
         if out is not None or row_idx is not None:
             return y
         return y.reshape(*shape[:-1], self.out_features)

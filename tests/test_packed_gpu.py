@@ -1,0 +1,151 @@
+"""GPU parity of the packed K64 layer path (pq_pack_k64, pq_quant_rows_packed, pq_int8_gemm_packed): the packed
+bytes equal the oracle's restatement of the layout (oracle.pack_k64), the packed quantizer equals the row-major
+quantizer packed, the packed GEMM's int32 accumulator is exact, and its fused output equals the row-major GEMM's
+bit for bit (same arithmetic, only the operand layout differs)."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import MAX_REL, MEAN_REL, bits, dcode, rel_errors
+
+pytestmark = pytest.mark.gpu
+
+
+def _codes(M, N, K, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    return a.to(dev), w.to(dev)
+
+
+@pytest.mark.parametrize("R,K", [(1, 64), (16, 64), (37, 192), (300, 640), (1000, 3072), (64, 12288)])
+def test_pack_k64_matches_oracle(oracle, cuda, R, K):
+    from pyraquant_amd import int8_exec as E
+
+    a, _ = _codes(R, 1, K, R + K, cuda)
+    p = E.pack_k64(a)
+    assert np.array_equal(p.cpu().numpy(), oracle.pack_k64(a.cpu().numpy()))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K", [(1, 3072), (15, 640), (17, 1280), (300, 3072), (33, 12288)])
+def test_quant_rows_packed(oracle, cuda, dtype, M, K):
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    x = make_x(M, K, dtype, seed=3 * M + K).to(cuda)
+    qp, s = E.quant_rows_packed(x)
+    qo, so = oracle.quant_rows(bits(x), dcode(dtype))
+    assert np.array_equal(qp.cpu().numpy(), oracle.pack_k64(qo))        # padding rows are zero too
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+def test_quant_rows_packed_gather_and_view(oracle, cuda):
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    base = make_x(500, 3072 + 12288, torch.bfloat16, seed=4).to(cuda)
+    x = base[:, 3072:]                                           # row-slice view, ldx = 15360
+    idx = torch.tensor([499, 0, 7, 7, 250, 31, 100], dtype=torch.int32)
+    qp, s = E.quant_rows_packed(x, idx.to(cuda))
+    qo, so = oracle.quant_rows(bits(x.contiguous()), 0, idx.numpy())
+    assert np.array_equal(qp.cpu().numpy(), oracle.pack_k64(qo))
+    assert np.array_equal(s.cpu().numpy(), so)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (7, 640, 640), (255, 256, 192), (257, 768, 1280),
+                                   (1000, 320, 3072), (513, 1280, 2560), (4096, 3072, 3072)])
+def test_gemm_packed_i32_exact(oracle, cuda, M, N, K):
+    from pyraquant_amd import int8_exec as E
+
+    a, w = _codes(M, N, K, M * 3 + N + K, cuda)
+    c = E.int8_gemm_packed(E.pack_k64(a), None, E.pack_k64(w), None, None, M, N, K, torch.int32)
+    assert np.array_equal(c.cpu().numpy(), oracle.gemm_i32(a.cpu().numpy(), w.cpu().numpy()))
+
+
+@pytest.mark.parametrize("lr", [0, 16, 32, 64])
+@pytest.mark.parametrize("M,N,K", [(333, 640, 1280), (1024, 3072, 3072), (77, 9216, 192)])
+def test_gemm_packed_equals_rowmajor(cuda, lr, M, N, K):
+    """Same fp32 epilogue on the same accumulators: bit-identical to the row-major kernel, with bias, low rank
+    and both output dtypes."""
+    from pyraquant_amd import int8_exec as E
+
+    a, w = _codes(M, N, K, 5 * M + lr, cuda)
+    g = torch.Generator().manual_seed(lr + 1)
+    s_row = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(cuda)
+    s_w = (torch.rand(N, generator=g) * 2e-4 + 1e-5).to(cuda)
+    bias = (torch.randn(N, generator=g) * 0.01).to(cuda)
+    for dt in (torch.bfloat16, torch.float16):
+        t = l2t = None
+        if lr:
+            t = (torch.randn(M, lr, generator=g) * 0.5).to(dt).to(cuda)
+            l2t = (torch.randn(N, lr, generator=g) * 0.02).to(dt).to(cuda)
+        ref = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, dt)
+        got = E.int8_gemm_packed(E.pack_k64(a), s_row, E.pack_k64(w), s_w, bias, M, N, K, dt, t=t, l2t=l2t)
+        assert torch.equal(got, ref), (dt, lr)
+
+
+def test_gemm_packed_scatter(oracle, cuda):
+    """Routed scatter on the packed path: gathered rows land in their canvas rows, other rows keep their bits."""
+    from pyraquant_amd import int8_exec as E
+
+    M, N, K, C = 300, 640, 640, 1000
+    a, w = _codes(M, N, K, 21, cuda)
+    g = torch.Generator().manual_seed(5)
+    s_row = torch.rand(M, generator=g) * 0.05 + 1e-3
+    s_w = torch.rand(N, generator=g) * 2e-4 + 1e-5
+    bias = (torch.randn(N, generator=g) * 0.01).float()
+    rows = torch.randperm(C, generator=g)[:M].to(torch.int32)
+    canvas = torch.randn(C, N, generator=g).to(torch.bfloat16)
+    before = bits(canvas)
+    out = canvas.to(cuda)
+    E.int8_gemm_packed(E.pack_k64(a), s_row.to(cuda), E.pack_k64(w), s_w.to(cuda), bias.to(cuda), M, N, K,
+                       torch.bfloat16, out=out, out_row_idx=rows.to(cuda))
+    acc = oracle.gemm_i32(a.cpu().numpy(), w.cpu().numpy())
+    ref = oracle.from_f32(oracle.epilogue_f32(acc, s_row.numpy(), s_w.numpy(), bias.numpy()), 0)
+    got = bits(out)
+    r = rows.numpy()
+    assert np.array_equal(got[r], ref)
+    keep = np.setdiff1d(np.arange(C), r)
+    assert np.array_equal(got[keep], before[keep])
+
+
+def test_gemm_packed_full_c1_checksum(oracle, cuda):
+    """c1 shape on the packed path: int64 row and column checksums of the int32 accumulator are exact, and 64
+    sampled rows match the oracle bit for bit."""
+    from pyraquant_amd import int8_exec as E
+
+    M, N, K = 65536, 12288, 3072
+    a, w = _codes(M, N, K, 42, cuda)
+    c = E.int8_gemm_packed(E.pack_k64(a), None, E.pack_k64(w), None, None, M, N, K, torch.int32)
+    rowsum = c.to(torch.int64).sum(dim=1)
+    expect = (a.to(torch.int64) * w.to(torch.int64).sum(dim=0)[None, :]).sum(dim=1)
+    assert torch.equal(rowsum, expect)
+    colsum = c.to(torch.int64).sum(dim=0)
+    expect_c = (w.to(torch.int64) * a.to(torch.int64).sum(dim=0)[None, :]).sum(dim=1)
+    assert torch.equal(colsum, expect_c)
+    g = torch.Generator().manual_seed(1)
+    sample = torch.randperm(M, generator=g)[:64].sort().values.to(cuda)
+    assert np.array_equal(c[sample].cpu().numpy(), oracle.gemm_i32(a[sample].cpu().numpy(), w.cpu().numpy()))
+
+
+@pytest.mark.parametrize("cfg,M", [("c0", 4096), ("c1", 777)])
+def test_int8linear_packed_path(oracle, cuda, cfg, M):
+    """Int8Linear.forward runs on the packed path for per-channel layers; output within the tolerance of the
+    oracle and equal to the row-major GEMM on the same codes."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import CONFIGS, make_linear, make_x
+
+    c = CONFIGS[cfg]
+    q = E.Int8Linear(make_linear(c.K, c.N, c.lowrank, c.bias), device=cuda)
+    assert q.weight_packed is not None
+    x = make_x(M, c.K).to(cuda)
+    y = q(x)
+    o = oracle.linear(bits(x), 0, q.weight_int8.cpu().numpy(), q.w_scale.cpu().numpy(), q.bias.cpu().numpy(), 0,
+                      bits(q.lr_A), bits(q.lr_B))
+    mx, mean = rel_errors(oracle.to_f32(bits(y), 0), o["y"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    xq, sx = E.quant_rows(x)
+    t = E.lowrank_down(x, q.lr_At)
+    ref = E._gemm(xq, sx, q.weight_int8, q.w_scale, 0, q.bias, t, q.lr_Bt, torch.bfloat16)
+    assert torch.equal(y, ref)
