@@ -34,6 +34,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=16384, help="row sample of the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run 3 device-to-device copies of BYTES (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE "
+                         "against a plain copy kernel of known size) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the INT8 executor "
@@ -50,6 +53,14 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe // 4, dtype=torch.int32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4}), flush=True)
+        return 0
     cfg = CONFIGS[args.config]
     lin = make_linear(cfg.K, cfg.N, cfg.lowrank, cfg.bias, dtype=cfg.dtype)
     q = E.Int8Linear(lin, device=dev, group_size=cfg.group)
@@ -111,6 +122,14 @@ def main() -> int:
     quant_gbs = quant_bytes / (quant_ms * 1e-3) / 1e9
     down_ms = avg_ms("down")
 
+    # HBM bytes per GEMM launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, copy-calibrated) for this config
+    traffic, traffic_src = None, None
+    prof = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"int8_gemm_{cfg.name}_traffic.json")
+    if os.path.exists(prof):
+        with open(prof) as fh:
+            traffic = json.load(fh).get("traffic_bytes")
+        traffic_src = os.path.relpath(prof, os.path.dirname(os.path.abspath(__file__)))
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, lin, args.cpu_rows, args.cpu_iters)
@@ -148,7 +167,8 @@ def main() -> int:
             "peak": INT8_PEAK_TOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "kernel": "int8_gemm (fused dequant + low-rank + bias epilogue)",
             "work_per_launch": f"2*M*N*K = {ops:.4e} int8 ops",
         },

@@ -9,7 +9,9 @@ restatement of the reference's arithmetic. Each function names the reference lin
 (paths relative to the PyraQuant repository). Arrays are numpy; 16-bit floats travel as their raw
 ``uint16`` bit patterns with a dtype code (``BF16`` / ``F16``).
 
-Pinning (what each function is checked against besides itself) is in ``oracle/README.md``.
+Each function is pinned by checks that do not restate it (``tests/test_oracle_cpu.py``): golden fixtures computed
+by torch's CPU operators on the reference's torch lines (``tests/golden/``), ``torch._int_mm``, exact-rational and
+float64 arithmetic, closed-form special cases and invariants. ``lowrank_down`` is pinned only to a tolerance.
 """
 from __future__ import annotations
 

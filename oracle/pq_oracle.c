@@ -10,7 +10,10 @@
  * no fast-math, SSE on x86-64), round-to-nearest-even; nearbyintf() is round half to even, the rounding
  * of torch.round.
  *
- * Pinning of each function (what checks it besides itself) is listed in oracle/README.md.
+ * Each function is pinned by checks that do not restate it (tests/test_oracle_cpu.py): golden fixtures computed by
+ * torch's CPU operators on the reference's torch lines (tests/golden/), torch._int_mm, exact-rational and float64
+ * arithmetic, closed-form special cases and invariants. lowrank_down is pinned only to a tolerance (the
+ * reference's library GEMM fixes no accumulation order).
  */
 #include <math.h>
 #include <stdint.h>

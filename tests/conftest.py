@@ -43,7 +43,7 @@ def cuda():
     return torch.device("cuda:0")
 
 
-# Tolerance of the floating-point outputs: against the oracle's fp32 result r computed
+# Tolerance of the floating-point outputs (the build's parity bar): against the oracle's fp32 result r computed
 # from the same int8 codes, max relative error max|y - r| / max|r| <= 1e-2 and mean relative error
 # sum|y - r| / sum|r| <= 5e-3. (An element-wise ratio is undefined where r crosses zero.)
 MAX_REL, MEAN_REL = 1e-2, 5e-3

@@ -104,7 +104,7 @@ def test_quant_rows_empty(cuda):
 
 @pytest.mark.parametrize("cfg", ["c1", "c2a"])
 def test_quant_rows_full_size(oracle, cuda, cfg):
-    """Full BASELINE shapes, bit-exact against the oracle."""
+    """Full c1 / c2a shapes, bit-exact against the oracle."""
     from pyraquant_amd.workloads import CONFIGS, make_x
 
     c = CONFIGS[cfg]
