@@ -9,10 +9,11 @@
 // column operand ("j") an activation row m, so each lane ends up holding 4 consecutive n of one output
 // row m (8-byte 16-bit stores) and needs one s_row value per 32 x 32 tile.
 //
-// Per-channel / int32 kernel (gemm_dma_kernel). 256 threads = 2 x 2 wavefronts, one wavefront per SIMD.
-// A workgroup owns a BN x BM (n x m) block, each wave a (BN/2) x (BM/2) quarter held as TI x TJ
-// v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in AGPRs; 256 of them for the 256 x 256 block).
-// K advances in stages of 64 bytes through a ring of NS LDS stages (5 x 32 KB for 256 x 256 blocks) filled by
+// Per-channel / int32 kernel (gemm_dma_kernel). 256 threads = 2 x 2 wavefronts. A workgroup owns a BN x BM (n x m)
+// block, each wave a (BN/2) x (BM/2) quarter held as TI x TJ v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in
+// AGPRs). Large problems run 256 x 128 blocks at two workgroups per CU (128 accumulators per wave, so two waves
+// share a SIMD and one workgroup's epilogue overlaps the other's MFMAs); small ones 128 x 128 at one per CU.
+// K advances in stages of 64 bytes through a ring of NS LDS stages (3 x 24 KB per workgroup at two per CU) filled by
 // LDS-DMA buffer loads (buffer_load_dwordx4 ... lds): no VGPR staging, no ds_write, and NS - 1 stages of
 // prefetch in flight to cover L2 / MALL latency. One DMA instruction fills 1 KB = 16 LDS rows of 64 bytes;
 // each lane fetches the 16-byte chunk that the XOR swizzle places at its LDS slot, so the MFMA operand reads
@@ -96,15 +97,17 @@ __device__ __forceinline__ int acc_read(int a) {
   return v;
 }
 
-template <int TI, int TJ, int MODE, int LRS, int LRDT, int ODT>
+template <int TI, int TJ, int MODE, int LRS, int LRDT, int ODT, int CB = 2>
 struct Epilogue {
+  // CB = 2: the column operands of weight tile i + 1 load while tile i is computed (one workgroup per CU);
+  // CB = 1: loaded right before use (two workgroups per CU hide the latency and the register budget is halved).
   static constexpr bool HAS_LR = LRS > 0;
   static constexpr int RS = HAS_LR ? LRS : 1;   // 16-wide slices of the low rank: R == 16 * LRS exactly
   float sr[TJ];
   int orow[TJ];
   v4i tv[TJ][RS];
-  v4f sc[2][4], bi[2][4];
-  v4i lb[2][RS];
+  v4f sc[CB][4], bi[CB][4];
+  v4i lb[CB][RS];
 
   __device__ __forceinline__ void load_cols(const GemmArgs& p, int slot, int ntile, int lane) {
     if constexpr (MODE != kModeI32) {
@@ -199,12 +202,16 @@ struct Epilogue {
 #pragma unroll
         for (int j = 0; j < TJ; ++j) srow[j * 32 + (lane & 31)] = orow[j];
       }
-      load_cols(p, 0, nbase, lane);
+      if constexpr (CB == 2) load_cols(p, 0, nbase, lane);
 #pragma unroll
       for (int i = 0; i < TI; ++i) {
-        if (i + 1 < TI) load_cols(p, (i + 1) & 1, nbase + (i + 1) * 32, lane);
+        if constexpr (CB == 2) {
+          if (i + 1 < TI) load_cols(p, (i + 1) & 1, nbase + (i + 1) * 32, lane);
+        } else {
+          load_cols(p, 0, nbase + i * 32, lane);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        const int c = i & 1;
+        const int c = CB == 2 ? (i & 1) : 0;
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
           v16f y;
@@ -273,8 +280,9 @@ __device__ __forceinline__ void wait_dma() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
 }
 
-template <int TI, int TJ, int NS, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
-__global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
+template <int TI, int TJ, int NS, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(OCC, OCC)))
+void gemm_dma_kernel(const GemmArgs p) {
   static_assert(MODE != kModeGroup32, "group-32 runs on gemm_reg_kernel");
   constexpr int BN = 64 * TI, BM = 64 * TJ;
   constexpr int WB = BN * kBKd, AB = BM * kBKd, STAGE = WB + AB;
@@ -283,7 +291,7 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
   constexpr int NF = TI + TJ;                 // fragments per substep
   constexpr int kRest = TI * TJ - NF;         // MFMAs of a substep beyond the NF that carry a fragment read
   constexpr int kVPer = kRest > 0 ? (DPW + kRest - 1) / (kRest > 0 ? kRest : 1) : 0;   // DMA per such MFMA
-  static_assert(NS >= 3 && NS * STAGE <= 160 * 1024, "LDS ring");
+  static_assert(NS >= 3 && NS * STAGE * OCC <= 160 * 1024, "LDS ring");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
 
   const int tid = threadIdx.x;
@@ -422,13 +430,13 @@ __global__ __launch_bounds__(256) void gemm_dma_kernel(const GemmArgs p) {
     b = bn;
   }
   // last stage: the epilogue's operands are fetched under its MFMAs
-  Epilogue<TI, TJ, MODE, LRS, LRDT, ODT> epi;
+  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT, OCC == 1 ? 2 : 1>;
+  Epi epi;
   const int nbase = n0 + wn * (BN / 2), mbase = m0 + wm * (BM / 2);
   epi.prefetch_rows(p, mbase, lane);
   rd(f1, b, 1);
   mm(f0);
   mm(f1);
-  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT>;
   static_assert(4 * Epi::kStageBytes <= NS * STAGE, "output staging must fit the LDS ring");
   wait_dma<0>();     // the out-of-range DMAs of the last iterations may still target the ring
   __syncthreads();   // every wave is done reading the ring: it becomes the output staging area
@@ -591,14 +599,20 @@ int grid_of(GemmArgs& a, int BM, int BN, dim3& grid) {
   return PQ_OK;
 }
 
-template <int TI, int TJ, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
+// Ring depth: as many 64-byte K stages as fit this workgroup's share of the 160 KB LDS (5 x 32 KB for 256 x 256
+// blocks at one workgroup per CU, 3 x 24 KB for 256 x 128 blocks at two per CU), at most 8.
+template <int TI, int TJ, int OCC>
+constexpr int ring_stages() {
+  return (160 * 1024 / OCC) / ((64 * TI + 64 * TJ) * kBKd) < 8 ? (160 * 1024 / OCC) / ((64 * TI + 64 * TJ) * kBKd) : 8;
+}
+
+template <int TI, int TJ, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 int launch_dma(GemmArgs& a, hipStream_t stream) {
-  // as many 64-byte K stages as fit the 160 KB LDS: 5 x 32 KB for 256 x 256 blocks, 8 x 16 KB for 128 x 128
-  constexpr int NS = TI * TJ >= 16 ? 5 : 8;
+  constexpr int NS = ring_stages<TI, TJ, OCC>();
   dim3 grid;
   const int st = grid_of(a, 64 * TJ, 64 * TI, grid);
   if (st != PQ_OK) return st;
-  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, NS, PACKED, MODE, LRS, LRDT, ODT>), grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, NS, OCC, PACKED, MODE, LRS, LRDT, ODT>), grid, dim3(256), 0, stream, a);
   return check_launch("int8_gemm");
 }
 
@@ -612,10 +626,12 @@ int launch_reg(GemmArgs& a, hipStream_t stream) {
   return check_launch("int8_gemm");
 }
 
-// Tile choice of the LDS-DMA kernel: 256 x 256 blocks when they fill the 256 CUs at least twice, else 128 x 128.
+// Tile choice of the LDS-DMA kernel: 256 x 128 (n x m) blocks at two workgroups per CU when they fill the 512
+// workgroup slots at least twice (one workgroup's epilogue, barriers and first-stage latency then overlap the other's
+// MFMAs), else 128 x 128 blocks at one per CU.
 inline bool big_tiles(const GemmArgs& a) {
-  const int64_t t256 = (int64_t)((a.M + 255) / 256) * ((a.N + 255) / 256);
-  return t256 >= 512;
+  const int64_t tiles = (int64_t)((a.M + 127) / 128) * ((a.N + 255) / 256);
+  return tiles >= 1024;
 }
 
 template <bool PACKED, int MODE, int LRS, int LRDT, int ODT>
@@ -625,8 +641,8 @@ int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
     static_assert(!PACKED, "group-32 takes row-major operands");
     return launch_reg<2, 2, 2, 2, MODE, LRS, LRDT, ODT>(a, stream);
   } else {
-    if (big_tiles(a)) return launch_dma<4, 4, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
-    return launch_dma<2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    if (big_tiles(a)) return launch_dma<4, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    return launch_dma<2, 2, 1, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
   }
 }
 
@@ -718,8 +734,8 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
   args.a = a; args.w = w; args.c = c;
   args.lda = lda; args.ldw = ldw; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
-  if (big_tiles(args)) return launch_dma<4, 4, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
-  return launch_dma<2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+  if (big_tiles(args)) return launch_dma<4, 2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+  return launch_dma<2, 2, 1, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
 }
 
 extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
@@ -743,8 +759,8 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
     if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 16)
       return set_error(PQ_EALIGN, "pq_int8_gemm_packed: int32 c must be 16-byte aligned with ldc %% 4 == 0");
     args.ldc = ldc;
-    if (big_tiles(args)) return launch_dma<4, 4, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
-    return launch_dma<2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+    if (big_tiles(args)) return launch_dma<4, 2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+    return launch_dma<2, 2, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
   }
   if (!s_row || !s_w) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null s_row / s_w");
   if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 8)

@@ -149,3 +149,31 @@ def test_int8linear_packed_path(oracle, cuda, cfg, M):
     t = E.lowrank_down(x, q.lr_At)
     ref = E._gemm(xq, sx, q.weight_int8, q.w_scale, 0, q.bias, t, q.lr_Bt, torch.bfloat16)
     assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(8191, 6464, 1280), (16400, 4160, 192)])
+def test_gemm_big_tile_path_ragged(oracle, cuda, M, N, K):
+    """Shapes with >= 1024 256 x 128 tiles take the two-workgroups-per-CU kernel; ragged M and N (tail tiles on
+    both edges) stay exact there, row-major and packed, and the fused outputs agree bit for bit."""
+    from pyraquant_amd import int8_exec as E
+
+    a, w = _codes(M, N, K, M + N, cuda)
+    c = E.int8_gemm_i32(a, w)
+    cp = E.int8_gemm_packed(E.pack_k64(a), None, E.pack_k64(w), None, None, M, N, K, torch.int32)
+    assert torch.equal(c, cp)
+    g = torch.Generator().manual_seed(1)
+    sample = torch.cat([torch.arange(M - 40, M), torch.randperm(M - 40, generator=g)[:24]]).sort().values.to(cuda)
+    assert np.array_equal(c[sample].cpu().numpy(), oracle.gemm_i32(a[sample].cpu().numpy(), w.cpu().numpy()))
+    s_row = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(cuda)
+    s_w = (torch.rand(N, generator=g) * 2e-4 + 1e-5).to(cuda)
+    bias = (torch.randn(N, generator=g) * 0.01).to(cuda)
+    t = (torch.randn(M, 32, generator=g) * 0.5).to(torch.bfloat16).to(cuda)
+    l2t = (torch.randn(N, 32, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    ref = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, torch.bfloat16)
+    got = E.int8_gemm_packed(E.pack_k64(a), s_row, E.pack_k64(w), s_w, bias, M, N, K, torch.bfloat16, t=t, l2t=l2t)
+    assert torch.equal(got, ref)
+    acc = c[sample].cpu().numpy()
+    yo = oracle.epilogue_f32(acc, s_row[sample].cpu().numpy(), s_w.cpu().numpy(), bias.cpu().numpy(),
+                             bits(t[sample]), bits(l2t.t().contiguous()), 0)
+    mx, mean = rel_errors(oracle.to_f32(bits(got[sample]), 0), yo)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
