@@ -4,7 +4,7 @@ up-projection (config c1: M=65536 tokens, K=3072, N=12288, rank-32 low-rank bran
 
 A step is the whole layer on inputs already resident in HBM, as Int8Linear.forward runs it: low-rank
 down-projection (t = x @ L1), per-token quantizer writing packed K64 codes, fused INT8 GEMM over packed operands
-+ dequant + low-rank up + bias epilogue (group-32 layers: row-major quantizer and GEMM). `value` = 2*M*N*K / step time (INT8 TOPS
++ dequant + low-rank up + bias epilogue (group-32 layers: per-group rescale in the GEMM's main loop). `value` = 2*M*N*K / step time (INT8 TOPS
 of the whole layer). `roofline` prices the dominant kernel (the fused GEMM) against the dense INT8 MFMA peak
 (5.0 POP/s) from HIP events recorded around every GEMM launch of the timed steps, on the stream it runs on.
 `cpu_baseline` times the reference's torch CPU quantize + int-matmul path (restated in oracle/torch_ref.py) on
@@ -86,8 +86,8 @@ def main() -> int:
         if q.weight_packed is not None:
             xq, sx = E.quant_rows_packed(x, rows)
             e2 = mark()
-            E.int8_gemm_packed(xq, sx, q.weight_packed, q.w_scale, q.bias, M, cfg.N, cfg.K, cfg.dtype, t=t,
-                               l2t=q.lr_Bt, out=out, out_row_idx=rows)
+            E.int8_gemm_packed(xq, sx, q.weight_packed, q._scale_k(), q.bias, M, cfg.N, cfg.K, cfg.dtype, t=t,
+                               l2t=q.lr_Bt, out=out, out_row_idx=rows, group=q.group_size)
         else:
             xq, sx = E.quant_rows(x, rows)
             e2 = mark()

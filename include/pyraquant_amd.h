@@ -94,11 +94,12 @@ int pq_quant_weight(const float* w, int64_t N, int64_t K, int64_t ldw, int64_t g
 /*
  * Low-rank down-projection t = x[rows] @ lr_A, fp32 accumulation, rounded to the 16-bit type of x.
  * Replaces `t = x2.to(self.lr_A.dtype) @ self.lr_A` (deploy/int8_exec.py:390; also :403).
- * x and l1t must have the same dtype. l1t is lr_A transposed ([R, K], K-contiguous). R % 16 == 0,
- * R <= 128, K % 8 == 0, 16-byte aligned x / l1t / t, ldx % 8 == 0, ldt % 8 == 0.
- * row_idx as in pq_quant_rows (the routed gather), or NULL.
+ * x is [x_rows, ldx] (the rows row_idx may name; without row_idx x_rows >= M). x and l1t must have the same dtype.
+ * l1t is lr_A transposed ([R, K], K-contiguous). R in {32, 64, 96, 128}, K % 8 == 0, 16-byte aligned x / l1t / t,
+ * ldx % 8 == 0, ldt % 8 == 0. row_idx as in pq_quant_rows (the routed gather), or NULL. K % 64 == 0 and R <= 64 take
+ * the LDS-DMA kernel (x streamed once in whole 128-byte row segments); other shapes a per-row-fragment kernel.
  */
-int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t ldx,
+int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
                     const int32_t* row_idx, const void* l1t, int64_t R, void* t, int64_t ldt,
                     hipStream_t stream);
 
@@ -135,14 +136,14 @@ int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
 
 /*
  * Fused INT8 GEMM over packed K64 operands (ap: activation codes [M, K], wp: weights [N, K], both in the packed
- * K64 layout). Same math, epilogue, scatter and requirements as pq_int8_gemm with group == 0; with
- * out_dtype == PQ_I32, c receives the raw int32 accumulator (s_row, s_w, bias, t, l2t, out_row_idx ignored;
- * c 16-byte aligned, ldc % 4 == 0). This is the layer path of Int8Linear: the quantizer writes ap directly
+ * K64 layout). Same math, epilogue, scatter and requirements as pq_int8_gemm (group 0: s_w [N]; group 32:
+ * s_w [K/32, N] group-major); with out_dtype == PQ_I32, c receives the raw int32 accumulator (s_row, s_w, group,
+ * bias, t, l2t, out_row_idx ignored; c 16-byte aligned, ldc % 4 == 0). This is the layer path of Int8Linear: the quantizer writes ap directly
  * (pq_quant_rows_packed) and the weights are packed once at conversion (pq_pack_k64).
  * Replaces `int8_gemm_fused` / `int8_gemm_lr` (deploy/int8_exec.py:202-212, 327-336) as called from
  * `Int8Linear.forward` (deploy/int8_exec.py:382-393).
  */
-int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
+int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w, int64_t group,
                         const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
                         void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t M, int64_t N,
                         int64_t K, hipStream_t stream);

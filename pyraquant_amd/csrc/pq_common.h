@@ -24,6 +24,18 @@ typedef unsigned short us2 __attribute__((ext_vector_type(2)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
+// ---- LDS-DMA helpers ---------------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (raw, 32-bit data format)
+
+// s_waitcnt vmcnt(N) (expcnt / lgkmcnt left at their maxima). The compiler does not count LDS-DMA loads as
+// LDS writes before a barrier, so every hand-over of a DMA-filled LDS stage waits for them explicitly.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+}
+
 // ---- packed K64 layout -----------------------------------------------------------------------------------------
 // Slot of 16-byte chunk c of row r' (0..15) of a 1 KB block is c ^ k64_swz(r'): among 8 consecutive rows the
 // (row parity, slot) pairs of one chunk are distinct, and among 16 consecutive rows the (row % 4, slot) pairs are,

@@ -9,7 +9,7 @@
 // column operand ("j") an activation row m, so each lane ends up holding 4 consecutive n of one output
 // row m (8-byte 16-bit stores) and needs one s_row value per 32 x 32 tile.
 //
-// Per-channel / int32 kernel (gemm_dma_kernel). 256 threads = 2 x 2 wavefronts. A workgroup owns a BN x BM (n x m)
+// The kernel (gemm_dma_kernel). 256 threads = 2 x 2 wavefronts. A workgroup owns a BN x BM (n x m)
 // block, each wave a (BN/2) x (BM/2) quarter held as TI x TJ v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in
 // AGPRs). Large problems run 256 x 128 blocks at two workgroups per CU (128 accumulators per wave, so two waves
 // share a SIMD and one workgroup's epilogue overlaps the other's MFMAs); small ones 128 x 128 at one per CU.
@@ -21,9 +21,11 @@
 // software-pipelined: the fragments of the next substep are read from LDS while the MFMAs of the current one
 // run, and the DMA of a new stage is interleaved with the MFMAs. One workgroup barrier per stage.
 //
-// Group-32 kernel (gemm_reg_kernel). Every 32-wide K group is one MFMA whose int32 partial the VALU scales
-// by s_w[g, n] into an fp32 accumulator (VGPRs); K advances in 64-byte stages through a register-staged
-// LDS double buffer.
+// Group-32 runs on the same kernel (MODE kModeGroup32): every 32-wide K substep is one K group, whose int32 partial
+// (one MFMA from zero) the VALU converts and fma's with s_w[g, n] into an fp32 accumulator held in VGPRs, groups in
+// order. The scales of each stage ride the DMA ring (dword LDS-DMA, a ring of NS + 1 slots of their own). That is
+// 16 converts + 16 FMAs per lane per MFMA (128 VALU cycles of a wave64 against 32 of the MFMA), so group-32 is
+// VALU-bound at a quarter of the INT8 MFMA rate; blocks are 128 x 128 at two workgroups per CU.
 //
 // Workgroup ids are remapped so that each XCD (ids are dealt round-robin over the 8 XCDs) walks a contiguous
 // run of tiles, rasterised in groups of GROUP_M m-tiles for L2 reuse.
@@ -35,7 +37,6 @@ namespace pq {
 namespace {
 
 constexpr int kGroupM = 8;                 // m-tiles per raster group
-constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (raw, 32-bit data format)
 constexpr int kOOB = 0x40000000;           // buffer offset beyond every operand's num_records (loads nothing)
 
 struct GemmArgs {
@@ -54,8 +55,6 @@ struct GemmArgs {
 };
 
 enum { kModeI32 = 0, kModeChannel = 1, kModeGroup32 = 2 };
-
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 // Map the linear workgroup id to (tile_m, tile_n): XCD-contiguous, then GROUP_M raster.
 __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -80,7 +79,7 @@ __device__ __forceinline__ v16f lr_mfma(v4i a, v4i b, v16f c) {
   }
 }
 
-// ---- epilogue shared by both kernels ----------------------------------------------------------------------
+// ---- epilogue ---------------------------------------------------------------------------------------
 // The wave's accumulators cover weight rows nbase + 32 i + [0, 32) and activation rows mbase + 32 j + [0, 32).
 // Lane holds, for tile (i, j) and register r: m = mbase + 32 j + lane % 32,
 // n = nbase + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4. The fp32 operations run in the reference's order
@@ -263,7 +262,7 @@ struct Epilogue {
   }
 };
 
-// ---- per-channel / int32 kernel: LDS-DMA ring of NS stages, 64-byte K stages ---------------------------------
+// ---- the GEMM kernel: LDS-DMA ring of NS stages, 64-byte K stages ---------------------------------
 constexpr int kBKd = 64;   // K bytes per stage (two 32-byte MFMA substeps)
 
 // LDS row r (64 bytes, one tile row) stores its 16-byte chunk c at slot c ^ swz(r). Among 8 consecutive rows the
@@ -272,27 +271,30 @@ constexpr int kBKd = 64;   // K bytes per stage (two 32-byte MFMA substeps)
 // 256-byte) bank window.
 __device__ __forceinline__ int swz(int r) { return k64_swz(r); }
 
-// s_waitcnt vmcnt(N) (expcnt / lgkmcnt left at their maxima). The compiler does not count LDS-DMA loads as
-// LDS writes before a barrier, so every stage hand-over waits for them explicitly.
 template <int N>
-__device__ __forceinline__ void wait_dma() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-}
+__device__ __forceinline__ void wait_dma() { wait_vmcnt<N>(); }
 
 template <int TI, int TJ, int NS, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(OCC, OCC)))
 void gemm_dma_kernel(const GemmArgs p) {
-  static_assert(MODE != kModeGroup32, "group-32 runs on gemm_reg_kernel");
+  constexpr bool G32 = MODE == kModeGroup32;
   constexpr int BN = 64 * TI, BM = 64 * TJ;
-  constexpr int WB = BN * kBKd, AB = BM * kBKd, STAGE = WB + AB;
+  constexpr int WB = BN * kBKd, AB = BM * kBKd;
+  constexpr int SB = G32 ? 2 * BN * 4 : 0;    // group-32: the stage's two scale rows s_w[g, n0 .. n0 + BN)
+  constexpr int STAGE = WB + AB;
+  // Group-32 scales have a ring of their own, one slot longer than the operand ring: stage s in slot s % (NS + 1).
+  // The DMA issued in iteration kt (stage kt + NS) then refills the slot of stage kt - 1, which every wave has
+  // finished reading before the barrier of iteration kt, so the MFMA substeps read their scales straight from LDS.
+  constexpr int SLOTS = NS + 1;
   constexpr int DW = BN / 64, DA = BM / 64;   // 1 KB DMA instructions per wave and stage (W, A)
-  constexpr int DPW = DW + DA;
+  constexpr int DS = SB / 256 / 4;            // 256-byte (dword) DMA instructions per wave and stage (scales)
+  constexpr int DPW = DW + DA + DS;
   constexpr int NF = TI + TJ;                 // fragments per substep
   constexpr int kRest = TI * TJ - NF;         // MFMAs of a substep beyond the NF that carry a fragment read
   constexpr int kVPer = kRest > 0 ? (DPW + kRest - 1) / (kRest > 0 ? kRest : 1) : 0;   // DMA per such MFMA
-  static_assert(NS >= 3 && NS * STAGE * OCC <= 160 * 1024, "LDS ring");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+  static_assert(NS >= 3 && (NS * STAGE + SLOTS * SB) * OCC <= 160 * 1024, "LDS ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE + SLOTS * SB];
+  uint8_t* const sscale = smem + NS * STAGE;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -340,9 +342,18 @@ void gemm_dma_kernel(const GemmArgs p) {
     sta = 16 * (int)p.lda;
   }
   constexpr int kStageStep = PACKED ? 1024 : kBKd;   // buffer offset of one K stage
+  // group-32 scales ([K/32, N] fp32): instruction i of this wave copies 64 scales of group 2 kt + d / (BN / 64),
+  // d = DS * wave + i, starting at n0 + 64 (d % (BN / 64))
+  __amdgpu_buffer_rsrc_t rs_s;
+  int vs = 0;
+  if constexpr (G32) {
+    rs_s = __builtin_amdgcn_make_buffer_rsrc((void*)p.s_w, (short)0, (p.K / 32) * p.N * 4, kBufferWord3);
+    vs = (n0 + lane) * 4;
+  }
 
-  auto dma = [&](int buf, int koff) {
+  auto dma = [&](int buf, int kt) {
     uint8_t* sb = smem + buf * STAGE;
+    const int koff = kt < KT ? kt * kStageStep : kOOB;
 #pragma unroll
     for (int i = 0; i < DW; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, (lds_void_t*)(sb + (wave * DW + i) * 1024), 16,
@@ -351,6 +362,15 @@ void gemm_dma_kernel(const GemmArgs p) {
     for (int i = 0; i < DA; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, (lds_void_t*)(sb + WB + (wave * DA + i) * 1024), 16,
                                                va + i * sta + koff, 0, 0, 0);
+    if constexpr (G32) {
+#pragma unroll
+      for (int i = 0; i < DS; ++i) {
+        const int d = wave * DS + i, g = d / (BN / 64), ch = d % (BN / 64);
+        const int so = kt < KT ? ((2 * kt + g) * p.N + ch * 64) * 4 : kOOB;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_s, (lds_void_t*)(sscale + (kt % SLOTS) * SB + g * BN * 4 + ch * 256),
+                                                 4, vs + so, 0, 0, 0);
+      }
+    }
   };
 
   // MFMA operand reads: lane reads tile row (lane % 32) of each 32-row fragment, K chunk 2 s + lane / 32 of
@@ -360,11 +380,12 @@ void gemm_dma_kernel(const GemmArgs p) {
   const int fw_off = (wn * (BN / 2) + (lane & 31)) * kBKd;
   const int fa_off = WB + (wm * (BM / 2) + (lane & 31)) * kBKd;
 
-  v16i acc[TI][TJ];
+  using acc_t = typename std::conditional<G32, v16f, v16i>::type;
+  acc_t acc[TI][TJ];
 #pragma unroll
   for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) acc[i][j] = v16i{};
+    for (int j = 0; j < TJ; ++j) acc[i][j] = acc_t{};
 
   v4i f0[NF], f1[NF];
   auto rd = [&](v4i (&f)[NF], int buf, int s) {
@@ -375,11 +396,31 @@ void gemm_dma_kernel(const GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < TJ; ++j) f[TI + j] = *reinterpret_cast<const v4i*>(sb + fa_off + j * 32 * kBKd + c);
   };
-  auto mm = [&](const v4i (&f)[NF]) {
+  // Per-channel / int32: MFMA accumulation in AGPRs. Group-32: substep s of stage kt is K group g = 2 kt + s; its
+  // int32 partial is converted and fma'd with s_w[g, n] into the fp32 accumulator, groups in order (deploy
+  // semantics: pyraquant/quantizers_weight.py:96-109). Lane element r of tile i holds row
+  // n = wn BN / 2 + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4.
+  auto mm = [&](const v4i (&f)[NF], int kt, int s) {
+    if constexpr (G32) {
+      const float* sg = reinterpret_cast<const float*>(sscale + (kt % SLOTS) * SB) + s * BN + wn * (BN / 2) + 4 * kh;
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+      for (int i = 0; i < TI; ++i) {
+        v4f s4[4];
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[TI + j], acc[i][j], 0, 0, 0);
+        for (int q = 0; q < 4; ++q) s4[q] = *reinterpret_cast<const v4f*>(sg + i * 32 + 8 * q);
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          const v16i part = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[TI + j], v16i{}, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(s4[r >> 2][r & 3], (float)part[r], acc[i][j][r]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[i], f[TI + j], acc[i][j], 0, 0, 0);
+    }
   };
 
   // Instruction order inside one substep: the NF fragment reads of the next substep are spread over the first NF
@@ -387,6 +428,10 @@ void gemm_dma_kernel(const GemmArgs p) {
   // ahead (issued after the reads: the scheduler keeps LDS reads ahead of a later LDS-DMA it cannot
   // disambiguate). sched_barrier(0) keeps each substep's MFMAs on its side of the stage barrier.
   auto interleave = [&](auto with_dma) {
+    if constexpr (G32) {
+      __builtin_amdgcn_sched_barrier(0);
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < NF; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
@@ -410,7 +455,7 @@ void gemm_dma_kernel(const GemmArgs p) {
   // must have landed at the barrier that ends iteration s - 1, NS - 1 iterations later; in between, the DMAs of
   // NS - 2 younger stages may still be in flight, hence vmcnt((NS - 2) * DPW).
 #pragma unroll
-  for (int st = 0; st < NS; ++st) dma(st, st < KT ? st * kStageStep : kOOB);
+  for (int st = 0; st < NS; ++st) dma(st, st);
   wait_dma<(NS - 1) * DPW>();
   __syncthreads();
   rd(f0, 0, 0);
@@ -418,14 +463,14 @@ void gemm_dma_kernel(const GemmArgs p) {
   for (int kt = 0; kt < KT - 1; ++kt) {
     const int bn = b + 1 == NS ? 0 : b + 1;
     rd(f1, b, 1);
-    mm(f0);
+    mm(f0, kt, 0);
     interleave(no_dma{});
     wait_dma<(NS - 2) * DPW>();   // this wave's DMA of stage kt + 1 has landed
     __syncthreads();              // every wave's has, and every wave is done reading buffer b
     __builtin_amdgcn_sched_barrier(0);
     rd(f0, bn, 0);
-    dma(b, kt + NS < KT ? (kt + NS) * kStageStep : kOOB);
-    mm(f1);
+    dma(b, kt + NS);
+    mm(f1, kt, 1);
     interleave(with_dma{});
     b = bn;
   }
@@ -435,158 +480,12 @@ void gemm_dma_kernel(const GemmArgs p) {
   const int nbase = n0 + wn * (BN / 2), mbase = m0 + wm * (BM / 2);
   epi.prefetch_rows(p, mbase, lane);
   rd(f1, b, 1);
-  mm(f0);
-  mm(f1);
+  mm(f0, KT - 1, 0);
+  mm(f1, KT - 1, 1);
   static_assert(4 * Epi::kStageBytes <= NS * STAGE, "output staging must fit the LDS ring");
   wait_dma<0>();     // the out-of-range DMAs of the last iterations may still target the ring
   __syncthreads();   // every wave is done reading the ring: it becomes the output staging area
   epi.run(p, acc, nbase, mbase, lane, smem + wave * Epi::kStageBytes);
-}
-
-// ---- group-32 kernel: register-staged LDS double buffer, 64-byte K stages ------------------------------------
-constexpr int kBK = 64;   // K bytes per stage
-
-// Byte offset of 16-byte chunk `chunk` of LDS row `row` (rows of 64 bytes, swizzled with row bits 1..2).
-__device__ __forceinline__ int lds_off(int row, int chunk) { return row * kBK + ((chunk ^ ((row >> 1) & 3)) << 4); }
-
-template <int WN, int WM, int TI, int TJ, int MODE, int LRS, int LRDT, int ODT>
-__global__ __attribute__((amdgpu_flat_work_group_size(WN * WM * 64, WN * WM * 64)))
-void gemm_reg_kernel(const GemmArgs p) {
-  constexpr int NT = WN * WM * 64;
-  constexpr int BN = WN * TI * 32;
-  constexpr int BM = WM * TJ * 32;
-  constexpr int CW = BN * kBK / 16 / NT;   // 16-byte chunks of W per thread per stage
-  constexpr int CA = BM * kBK / 16 / NT;   // 16-byte chunks of A per thread per stage
-  static_assert(CW * NT * 16 == BN * kBK && CA * NT * 16 == BM * kBK, "tile / thread mismatch");
-  constexpr int ROWS_PER_PASS = NT / 4;    // 4 chunks per 64-byte row
-
-  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT>;
-  constexpr int kRing = (BN + BM) * kBK;                                        // one stage of the double buffer
-  constexpr int kSmem = 2 * kRing > WN * WM * Epi::kStageBytes ? 2 * kRing : WN * WM * Epi::kStageBytes;
-  __shared__ __attribute__((aligned(16))) uint8_t smem_raw[kSmem];
-  uint8_t(*smem)[kRing] = reinterpret_cast<uint8_t(*)[kRing]>(smem_raw);
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wn = wave % WN;
-  const int wm = wave / WN;
-
-  int tm, tn;
-  tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
-  const int m0 = tm * BM;
-  const int n0 = tn * BN;
-
-  // Global -> register loaders. Thread owns chunk (tid % 4) of rows tid / 4 + ROWS_PER_PASS * i; the whole
-  // offset (row, K stage) is in the per-lane voffset, so rows past M / N fall outside num_records and load
-  // as zeros.
-  const int lrow = tid >> 2;
-  const int lchunk = tid & 3;
-  const int rows_w = min(BN, p.N - n0), rows_a = min(BM, p.M - m0);
-  const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.w + (int64_t)n0 * p.ldw), (short)0, (int)(rows_w * p.ldw), kBufferWord3);
-  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(p.a + (int64_t)m0 * p.lda), (short)0, (int)(rows_a * p.lda), kBufferWord3);
-  const int vo_w = lrow * (int)p.ldw + lchunk * 16;
-  const int vo_a = lrow * (int)p.lda + lchunk * 16;
-  const int pass_w = ROWS_PER_PASS * (int)p.ldw;
-  const int pass_a = ROWS_PER_PASS * (int)p.lda;
-  const int st_off = lds_off(lrow, lchunk);   // + i * ROWS_PER_PASS * kBK (row bits 1..2 unchanged)
-  static_assert((ROWS_PER_PASS & 7) == 0, "rows per pass must keep the swizzle bits");
-
-  const int rsub = lane & 31;
-  const int khalf = lane >> 5;
-
-  using acc_t = typename std::conditional<MODE == kModeGroup32, v16f, v16i>::type;
-  acc_t acc[TI][TJ];
-#pragma unroll
-  for (int i = 0; i < TI; ++i)
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) acc[i][j] = acc_t{};
-
-  v4i rw[CW], ra[CA];
-#pragma unroll
-  for (int i = 0; i < CW; ++i) rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, vo_w + i * pass_w, 0, 0);
-#pragma unroll
-  for (int i = 0; i < CA; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_a, vo_a + i * pass_a, 0, 0);
-  {
-    uint8_t* sw = smem[0];
-    uint8_t* sa = smem[0] + BN * kBK;
-#pragma unroll
-    for (int i = 0; i < CW; ++i) *reinterpret_cast<v4i*>(sw + st_off + i * ROWS_PER_PASS * kBK) = rw[i];
-#pragma unroll
-    for (int i = 0; i < CA; ++i) *reinterpret_cast<v4i*>(sa + st_off + i * ROWS_PER_PASS * kBK) = ra[i];
-  }
-  __syncthreads();
-
-  const int KT = p.K / kBK;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < KT;
-    if (more) {
-      const int ko = (kt + 1) * kBK;
-#pragma unroll
-      for (int i = 0; i < CW; ++i) rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_w, vo_w + ko + i * pass_w, 0, 0);
-#pragma unroll
-      for (int i = 0; i < CA; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rs_a, vo_a + ko + i * pass_a, 0, 0);
-    }
-    const uint8_t* sw = smem[buf];
-    const uint8_t* sa = smem[buf] + BN * kBK;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      v4i fw[TI], fa[TJ];
-      const int chunk = kk * 2 + khalf;
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-        fw[i] = *reinterpret_cast<const v4i*>(sw + lds_off(wn * TI * 32 + i * 32 + rsub, chunk));
-#pragma unroll
-      for (int j = 0; j < TJ; ++j)
-        fa[j] = *reinterpret_cast<const v4i*>(sa + lds_off(wm * TJ * 32 + j * 32 + rsub, chunk));
-      if constexpr (MODE == kModeGroup32) {
-        // one 32-wide K group per MFMA: int32 partial -> fp32, fma with the group scale of each row n
-        const int g = kt * 2 + kk;
-        const float* sg = p.s_w + (int64_t)g * p.N;
-#pragma unroll
-        for (int i = 0; i < TI; ++i) {
-          const int nb = n0 + wn * TI * 32 + i * 32 + 4 * khalf;
-          v4f s4[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int n = min(nb + 8 * q, p.N - 4);
-            s4[q] = *reinterpret_cast<const v4f*>(sg + n);
-          }
-#pragma unroll
-          for (int j = 0; j < TJ; ++j) {
-            const v16i part = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[i], fa[j], v16i{}, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const float sc = s4[r >> 2][r & 3];
-              acc[i][j][r] = __builtin_fmaf(sc, (float)part[r], acc[i][j][r]);
-            }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-          for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fw[i], fa[j], acc[i][j], 0, 0, 0);
-      }
-    }
-    if (more) {
-      uint8_t* nw = smem[buf ^ 1];
-      uint8_t* na = smem[buf ^ 1] + BN * kBK;
-#pragma unroll
-      for (int i = 0; i < CW; ++i) *reinterpret_cast<v4i*>(nw + st_off + i * ROWS_PER_PASS * kBK) = rw[i];
-#pragma unroll
-      for (int i = 0; i < CA; ++i) *reinterpret_cast<v4i*>(na + st_off + i * ROWS_PER_PASS * kBK) = ra[i];
-    }
-    __syncthreads();
-  }
-
-  Epi epi;
-  epi.prefetch_rows(p, m0 + wm * TJ * 32, lane);
-  __syncthreads();   // the LDS double buffer becomes the output staging area
-  epi.run(p, acc, n0 + wn * TI * 32, m0 + wm * TJ * 32, lane, smem_raw + wave * Epi::kStageBytes);
 }
 
 // ---- launchers ---------------------------------------------------------------------------------------------
@@ -601,28 +500,20 @@ int grid_of(GemmArgs& a, int BM, int BN, dim3& grid) {
 
 // Ring depth: as many 64-byte K stages as fit this workgroup's share of the 160 KB LDS (5 x 32 KB for 256 x 256
 // blocks at one workgroup per CU, 3 x 24 KB for 256 x 128 blocks at two per CU), at most 8.
-template <int TI, int TJ, int OCC>
+template <int TI, int TJ, int OCC, int MODE>
 constexpr int ring_stages() {
-  return (160 * 1024 / OCC) / ((64 * TI + 64 * TJ) * kBKd) < 8 ? (160 * 1024 / OCC) / ((64 * TI + 64 * TJ) * kBKd) : 8;
+  constexpr int stage = (64 * TI + 64 * TJ) * kBKd, sb = MODE == kModeGroup32 ? 2 * 64 * TI * 4 : 0;
+  constexpr int ns = (160 * 1024 / OCC - sb) / (stage + sb);   // NS operand stages + NS + 1 scale slots
+  return ns < 8 ? ns : 8;
 }
 
 template <int TI, int TJ, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 int launch_dma(GemmArgs& a, hipStream_t stream) {
-  constexpr int NS = ring_stages<TI, TJ, OCC>();
+  constexpr int NS = ring_stages<TI, TJ, OCC, MODE>();
   dim3 grid;
   const int st = grid_of(a, 64 * TJ, 64 * TI, grid);
   if (st != PQ_OK) return st;
   hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, NS, OCC, PACKED, MODE, LRS, LRDT, ODT>), grid, dim3(256), 0, stream, a);
-  return check_launch("int8_gemm");
-}
-
-template <int WN, int WM, int TI, int TJ, int MODE, int LRS, int LRDT, int ODT>
-int launch_reg(GemmArgs& a, hipStream_t stream) {
-  dim3 grid;
-  const int st = grid_of(a, WM * TJ * 32, WN * TI * 32, grid);
-  if (st != PQ_OK) return st;
-  hipLaunchKernelGGL((gemm_reg_kernel<WN, WM, TI, TJ, MODE, LRS, LRDT, ODT>), grid, dim3(WN * WM * 64), 0,
-                     stream, a);
   return check_launch("int8_gemm");
 }
 
@@ -637,9 +528,8 @@ inline bool big_tiles(const GemmArgs& a) {
 template <bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
   if constexpr (MODE == kModeGroup32) {
-    // fp32 accumulators live in VGPRs (the VALU rescales them every group): 2 x 2 waves of 64 x 64
-    static_assert(!PACKED, "group-32 takes row-major operands");
-    return launch_reg<2, 2, 2, 2, MODE, LRS, LRDT, ODT>(a, stream);
+    // fp32 accumulators live in VGPRs (the VALU rescales them every group): 128 x 128 blocks, two per CU
+    return launch_dma<2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
   } else {
     if (big_tiles(a)) return launch_dma<4, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
     return launch_dma<2, 2, 1, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
@@ -739,7 +629,7 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
 }
 
 extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
-                                   const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R,
+                                   int64_t group, const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R,
                                    int32_t lr_dtype, void* c, int64_t ldc, int32_t out_dtype,
                                    const int32_t* out_row_idx, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   if (M < 0 || N < 1 || K < 1) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: bad shape");
@@ -763,6 +653,8 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
     return launch_dma<2, 2, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
   }
   if (!s_row || !s_w) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null s_row / s_w");
+  if (group != 0 && group != 32)
+    return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: group must be 0 or 32, got %lld", (long long)group);
   if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 8)
     return set_error(PQ_EALIGN, "pq_int8_gemm_packed: c must be 8-byte aligned with ldc >= N, ldc %% 4 == 0");
   if ((uintptr_t)s_w % 16 || (bias && (uintptr_t)bias % 16))
@@ -779,5 +671,6 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
   args.t = static_cast<const uint16_t*>(t); args.l2t = static_cast<const uint16_t*>(l2t);
   args.out_row_idx = out_row_idx;
   args.ldt = ldt; args.ldc = ldc; args.R = (int)R;
+  if (group == 32) return dispatch_dtypes<true, kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
   return dispatch_dtypes<true, kModeChannel>(args, has_lr, lr_dtype, out_dtype, stream);
 }

@@ -290,6 +290,108 @@ __global__ __launch_bounds__(256) void pack_k64_kernel(const int8_t* __restrict_
   *reinterpret_cast<v4i*>(dst + t * 16) = v;
 }
 
+// ---- low-rank down-projection over an LDS-DMA ring (K % 64 == 0) ------------------------------------------------
+// t[m, :] = x[src(m), :] @ L1 with src(m) = row_idx ? row_idx[m] : m. A workgroup (4 waves) owns 128 output rows,
+// 32 per wave; K streams in 64-element (128-byte) stages through a 4-stage LDS ring filled by LDS-DMA: 128 rows of
+// x plus the R rows of l1t (= L1^T) for the stage. One DMA instruction fills 8 LDS rows of 128 bytes (each lane the
+// 16-byte chunk the swizzle puts at its slot), so every request is a whole row segment and x is read exactly once.
+// Per 16-wide K step a wave does R / 32 bf16/fp16 MFMA 32x32x16 with D[r][m] = sum_k l1t[r, k] x[m, k] (fp32), then
+// rounds to the 16-bit type (round to nearest even).
+constexpr int kLrRows = 128;
+constexpr int kLrNS = 4;
+
+__device__ __forceinline__ int lr_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+template <int DT, int RB>
+__global__ __launch_bounds__(256) void lowrank_down_dma_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int K, int64_t M, const int32_t* __restrict__ row_idx,
+    const uint16_t* __restrict__ l1t, uint16_t* __restrict__ t, int64_t ldt) {
+  constexpr int XB = kLrRows * 128, LB = RB * 32 * 128, STAGE = XB + LB;
+  constexpr int DPW = 4 + RB;   // DMA instructions per wave and stage: 4 for x, RB for l1t
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kLrNS * STAGE];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t m0 = (int64_t)blockIdx.x * kLrRows;
+  const int KT = K / 64;
+
+  const __amdgpu_buffer_rsrc_t rs_x = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, (int)(x_rows * ldx * 2), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rs_l = __builtin_amdgcn_make_buffer_rsrc((void*)l1t, (short)0, RB * 32 * K * 2, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rs_none = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, 0, kBufferWord3);
+
+  // x: instruction i fills rows (4 wave + i) * 8 + lane / 8 of the block; row % 8 = lane / 8 and row / 8 % 2 = i % 2
+  int vx[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = min(m0 + (wave * 4 + i) * 8 + (lane >> 3), M - 1);
+    const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
+    vx[i] = (int)(src * ldx * 2) + (((lane & 7) ^ (lane >> 3) ^ (i & 1)) << 4);
+  }
+  // l1t: instruction j fills rows 32 j + 8 wave + lane / 8; row % 8 = lane / 8 and row / 8 % 2 = wave % 2
+  const int vl = ((wave * 8 + (lane >> 3)) * K) * 2 + (((lane & 7) ^ (lane >> 3) ^ (wave & 1)) << 4);
+
+  auto dma = [&](int buf, int kt) {
+    uint8_t* sb = smem + buf * STAGE;
+    const bool live = kt < KT;   // past the end of K: a zero-size descriptor, the loads read nothing
+    const __amdgpu_buffer_rsrc_t rx = live ? rs_x : rs_none;
+    const __amdgpu_buffer_rsrc_t rl = live ? rs_l : rs_none;
+    const int ko = live ? kt * 128 : 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(sb + (wave * 4 + i) * 1024), 16, vx[i] + ko, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_void_t*)(sb + XB + (j * 4 + wave) * 1024), 16,
+                                               vl + j * 32 * K * 2 + ko, 0, 0, 0);
+  };
+
+  const int sw = (lane & 7) ^ ((lane >> 3) & 1);
+  const int kh = lane >> 5;
+  const int xo = (wave * 32 + (lane & 31)) * 128;
+  const int lo = XB + (lane & 31) * 128;
+  v16f acc[RB];
+#pragma unroll
+  for (int j = 0; j < RB; ++j) acc[j] = v16f{};
+
+#pragma unroll
+  for (int st = 0; st < kLrNS; ++st) dma(st, st);
+  wait_vmcnt<(kLrNS - 1) * DPW>();
+  __syncthreads();
+  int b = 0;
+  for (int kt = 0; kt < KT; ++kt) {
+    const uint8_t* sb = smem + b * STAGE;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = ((2 * s + kh) ^ sw) << 4;
+      const v4i xf = *reinterpret_cast<const v4i*>(sb + xo + c);
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        const v4i lf = *reinterpret_cast<const v4i*>(sb + lo + j * 32 * 128 + c);
+        if constexpr (DT == PQ_BF16) {
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, lf), __builtin_bit_cast(v8bf, xf), acc[j], 0, 0, 0);
+        } else {
+          acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, lf), __builtin_bit_cast(v8h, xf), acc[j], 0, 0, 0);
+        }
+      }
+    }
+    wait_vmcnt<(kLrNS - 2) * DPW>();   // this wave's DMA of stage kt + 1 has landed
+    __syncthreads();                    // every wave's has, and every wave is done reading buffer b
+    dma(b, kt + kLrNS);
+    b = b + 1 == kLrNS ? 0 : b + 1;
+  }
+  wait_vmcnt<0>();
+  // D[r][m]: lane holds row m = wave * 32 + lane % 32 and r = 32 j + 8 q + 4 (lane / 32) + (0..3)
+  const int64_t m = m0 + wave * 32 + (lane & 31);
+  if (m < M) {
+    uint16_t* trow = t + m * ldt + 4 * kh;
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<v2u*>(trow + j * 32 + 8 * q) =
+            v2u{pack2<DT>(acc[j][4 * q + 0], acc[j][4 * q + 1]), pack2<DT>(acc[j][4 * q + 2], acc[j][4 * q + 3])};
+  }
+}
+
 // ---- dequant epilogue over a materialised int32 accumulator ----------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(256) void dequant_epilogue_kernel(
@@ -367,7 +469,7 @@ extern "C" int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, i
   return set_error(PQ_EDTYPE, "pq_quant_rows_packed: unsupported dtype code %d", (int)x_dtype);
 }
 
-extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t ldx,
+extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
                                const int32_t* row_idx, const void* l1t, int64_t R, void* t, int64_t ldt,
                                hipStream_t stream) {
   if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_lowrank_down: bad shape");
@@ -377,6 +479,8 @@ extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t 
     return set_error(PQ_ESHAPE, "pq_lowrank_down: rank R=%lld must be 32, 64, 96 or 128", (long long)R);
   if (K % 8 != 0 || ldx < K || ldx % 8 != 0 || ldt < R || ldt % 8 != 0)
     return set_error(PQ_ESHAPE, "pq_lowrank_down: need K %% 8 == 0, ldx %% 8 == 0, ldt %% 8 == 0");
+  if (x_rows < 1 || (!row_idx && x_rows < M))
+    return set_error(PQ_ESHAPE, "pq_lowrank_down: x_rows=%lld must cover the rows read", (long long)x_rows);
   if ((uintptr_t)x % 16 || (uintptr_t)l1t % 16 || (uintptr_t)t % 16)
     return set_error(PQ_EALIGN, "pq_lowrank_down: x, l1t, t must be 16-byte aligned");
   if (dtype != PQ_BF16 && dtype != PQ_F16) return set_error(PQ_EDTYPE, "pq_lowrank_down: bad dtype %d", (int)dtype);
@@ -384,6 +488,17 @@ extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t 
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* lp = static_cast<const uint16_t*>(l1t);
   uint16_t* tp = static_cast<uint16_t*>(t);
+  // LDS-DMA kernel when K streams in whole 64-element stages and every byte offset fits the 32-bit buffer range
+  if (K % 64 == 0 && x_rows * ldx * 2 + 128 <= 0x7fffffffLL && R * K * 2 <= 0x7fffffffLL) {
+#define PQ_LRDMA(D, RB)                                                                                     \
+    if (dtype == D && R == RB * 32) {                                                                       \
+      hipLaunchKernelGGL((lowrank_down_dma_kernel<D, RB>), grid, block, 0, stream, xp, ldx, x_rows, (int)K, \
+                         M, row_idx, lp, tp, ldt);                                                          \
+      return check_launch("lowrank_down");                                                                  \
+    }
+    PQ_LRDMA(PQ_BF16, 1) PQ_LRDMA(PQ_BF16, 2) PQ_LRDMA(PQ_F16, 1) PQ_LRDMA(PQ_F16, 2)
+#undef PQ_LRDMA
+  }
 #define PQ_LRCASE(D, RB)                                                                                    \
   if (dtype == D && R == RB * 32) {                                                                         \
     hipLaunchKernelGGL((lowrank_down_kernel<D, RB>), grid, block, 0, stream, xp, ldx, (int)K, M, row_idx,  \

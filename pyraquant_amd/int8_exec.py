@@ -101,7 +101,7 @@ def lowrank_down(x2: torch.Tensor, lr_At: torch.Tensor, row_idx: Optional[torch.
     M = rows if ri is None else ri.shape[0]
     t = torch.empty((M, R), dtype=x2.dtype, device=x2.device)
     L = _lib.load()
-    _lib.check(L.pq_lowrank_down(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), _lib.ptr(ri),
+    _lib.check(L.pq_lowrank_down(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), rows, _lib.ptr(ri),
                                  _lib.ptr(lr_At), R, _lib.ptr(t), R, _lib.stream_of(x2.device)), "lowrank_down")
     return t
 
@@ -231,9 +231,11 @@ def quant_rows_packed(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) 
 def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor, w_scale: torch.Tensor,
                      bias: Optional[torch.Tensor], M: int, N: int, K: int, out_dtype: torch.dtype, *,
                      t: Optional[torch.Tensor] = None, l2t: Optional[torch.Tensor] = None,
-                     out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None,
+                     group: int = 0) -> torch.Tensor:
     """The fused GEMM over packed K64 operands (pq_int8_gemm_packed): xq_p from quant_rows_packed, w_p from
-    pack_k64. out_dtype torch.int32 returns the raw accumulator."""
+    pack_k64. group 0: w_scale [N]; group 32: w_scale [K/32, N] (group-major). out_dtype torch.int32 returns the
+    raw accumulator."""
     assert xq_p.dtype == torch.int8 and w_p.dtype == torch.int8
     _check_cuda(xq_p, s_row, w_p, w_scale, bias, t, l2t, out, out_row_idx)
     assert xq_p.numel() >= packed_rows(M) * K and w_p.numel() >= packed_rows(N) * K
@@ -241,12 +243,14 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
     L = _lib.load()
     if out_dtype == torch.int32:
         c = torch.empty((M, N), dtype=torch.int32, device=xq_p.device)
-        _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), None, None, None, None, 0, None, 0, 0,
+        _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), None, None, 0, None, None, 0, None, 0, 0,
                                          _lib.ptr(c), N, _lib.PQ_I32, None, M, N, K, _lib.stream_of(xq_p.device)),
                    "int8_gemm_packed")
         return c
     assert s_row.dtype == torch.float32 and s_row.is_contiguous() and s_row.numel() >= M
-    assert w_scale.dtype == torch.float32 and w_scale.is_contiguous() and w_scale.numel() == N
+    assert group in (0, 32), group
+    assert w_scale.dtype == torch.float32 and w_scale.is_contiguous()
+    assert w_scale.numel() == (N * K // 32 if group else N), (tuple(w_scale.shape), N, K, group)
     if bias is not None:
         assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == N
     if ori is not None:
@@ -262,7 +266,7 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
         R = t.shape[1]
         assert l2t.shape == (N, R), (tuple(l2t.shape), (N, R))
         lr_code, ldt = _lib.dtype_code(t.dtype), t.stride(0)
-    _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), _lib.ptr(s_row), _lib.ptr(w_scale),
+    _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), _lib.ptr(s_row), _lib.ptr(w_scale), group,
                                      _lib.ptr(bias), _lib.ptr(t), ldt, _lib.ptr(l2t), R, lr_code, _lib.ptr(out),
                                      out.stride(0), _lib.dtype_code(out_dtype), _lib.ptr(ori), M, N, K,
                                      _lib.stream_of(xq_p.device)), "int8_gemm_packed")
@@ -324,8 +328,8 @@ class Int8Linear(nn.Module):
         self.register_buffer("weight_int8", q)
         self.register_buffer("w_scale", s)
         N, K = q.shape
-        # per-channel layers whose shape the packed GEMM takes run on the packed K64 path
-        if not group_size and K % 64 == 0 and N % 64 == 0:
+        # layers whose shape the packed GEMM takes (per-channel and group-32) run on the packed K64 path
+        if K % 64 == 0 and N % 64 == 0:
             self.register_buffer("weight_packed", pack_k64(q))
         else:
             self.weight_packed = None
@@ -386,9 +390,9 @@ class Int8Linear(nn.Module):
                 t = t.to(x2.dtype)
         if self.weight_packed is not None:
             xq, sx = quant_rows_packed(x2, row_idx)
-            y = int8_gemm_packed(xq, sx, self.weight_packed, self.w_scale, self.bias, sx.shape[0], self.out_features,
-                                 self.in_features, x2.dtype, t=t, l2t=self._lr_bt(x2.dtype), out=out,
-                                 out_row_idx=out_row_idx)
+            y = int8_gemm_packed(xq, sx, self.weight_packed, self._scale_k(), self.bias, sx.shape[0],
+                                 self.out_features, self.in_features, x2.dtype, t=t, l2t=self._lr_bt(x2.dtype),
+                                 out=out, out_row_idx=out_row_idx, group=self.group_size)
         else:
             xq, sx = quant_rows(x2, row_idx)
             y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, t,

@@ -79,7 +79,8 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert lib.pq_int8_gemm_i32(p16, 128, p16, 128, nul, 128, 8, 128, 128, nul) == L.PQ_EINVAL
     assert lib.pq_quant_weight(nul, 4, 64, 64, 0, nul, nul, nul) == L.PQ_EINVAL
     assert lib.pq_quant_weight(p16, 4, 64, 64, 48, p16, p16, nul) == L.PQ_ESHAPE
-    assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, nul, p16, 24, p16, 32, nul) == L.PQ_ESHAPE
+    assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, 8, nul, p16, 24, p16, 32, nul) == L.PQ_ESHAPE
+    assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, 4, nul, p16, 32, p16, 32, nul) == L.PQ_ESHAPE   # x_rows < M
     assert lib.pq_dequant_epilogue(nul, nul, nul, nul, nul, 128, 0, 8, 128, nul) == L.PQ_EINVAL
 
 

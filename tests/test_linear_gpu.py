@@ -187,3 +187,31 @@ def test_backend_api():
     with pytest.raises(ValueError):
         E.set_backend("cublas")
     E.set_backend(E.DEFAULT_BACKEND)
+
+
+@pytest.mark.parametrize("M,K,R,gather", [(4096, 3072, 32, False), (1000, 3072, 64, False), (777, 1280, 32, True),
+                                          (129, 12288, 32, True), (64, 520, 32, False)])
+def test_lowrank_down_dma_and_fallback(oracle, cuda, M, K, R, gather):
+    """K % 64 == 0 and R <= 64 run the LDS-DMA kernel (also with a gather list holding duplicates and through a
+    row-slice view); K = 520 runs the per-fragment kernel. Both within bf16 rounding of the float64 product."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    rows = M + 37 if gather else M
+    base = make_x(rows, K + 64, seed=K + R).to(cuda)
+    x = base[:, 64:]                                            # row-slice view: ldx = K + 64
+    g = torch.Generator().manual_seed(R + K)
+    l1 = (torch.randn(K, R, generator=g) * 0.02).to(torch.bfloat16)
+    idx = None
+    if gather:
+        idx = torch.randint(0, rows, (M,), generator=g, dtype=torch.int32)
+        idx[:3] = torch.tensor([rows - 1, 0, 0], dtype=torch.int32)
+    t = E.lowrank_down(x, l1.t().contiguous().to(cuda), None if idx is None else idx.to(cuda))
+    xs = x.cpu()[idx.long()] if gather else x.cpu()
+    ref64 = xs.double() @ l1.double()
+    got = t.cpu().double()
+    err = (got - ref64).abs() / ref64.abs().clamp_min(1e-3 * ref64.abs().max())
+    assert float(err.max()) <= 1.5e-2, float(err.max())
+    ref_bits = oracle.lowrank_down(bits(x.contiguous()), 0, bits(l1), None if idx is None else idx.numpy())
+    mx, mean = rel_errors(oracle.to_f32(bits(t), 0), oracle.to_f32(ref_bits, 0))
+    assert mx <= MAX_REL * 2 and mean <= MEAN_REL, (mx, mean)

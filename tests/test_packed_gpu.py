@@ -177,3 +177,60 @@ def test_gemm_big_tile_path_ragged(oracle, cuda, M, N, K):
                              bits(t[sample]), bits(l2t.t().contiguous()), 0)
     mx, mean = rel_errors(oracle.to_f32(bits(got[sample]), 0), yo)
     assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (200, 1280, 1280), (513, 640, 2048), (64, 5120, 1280),
+                                   (300, 640, 5120), (4107, 320, 192)])
+def test_gemm_packed_group32_exact(oracle, cuda, M, N, K):
+    """Group-32 on the packed path: per-group int32 partials fma'd in group order, bit-exact against the oracle
+    and equal to the row-major kernel's output."""
+    from pyraquant_amd import int8_exec as E
+
+    a, w = _codes(M, N, K, 11 * M + K, cuda)
+    G = K // 32
+    g = torch.Generator().manual_seed(M + N)
+    s_row = torch.rand(M, generator=g) * 0.05 + 1e-3
+    s_w = torch.rand(N, G, generator=g) * 2e-4 + 1e-5       # [N, G], the reference's qdq layout
+    bias = (torch.randn(N, generator=g) * 0.01).float()
+    s_gn = s_w.t().contiguous().to(cuda)
+    y = E.int8_gemm_packed(E.pack_k64(a), s_row.to(cuda), E.pack_k64(w), s_gn, bias.to(cuda), M, N, K,
+                           torch.float16, group=32)
+    part = oracle.gemm_group_i32(a.cpu().numpy(), w.cpu().numpy(), 32)
+    ref = oracle.from_f32(oracle.epilogue_f32(part, s_row.numpy(), s_w.numpy(), bias.numpy()), 1)
+    mism = int((bits(y) != ref).sum())
+    assert mism == 0, f"{mism} of {ref.size} outputs differ"
+    y_rm = E._gemm(a, s_row.to(cuda), w, s_gn, 32, bias.to(cuda), None, None, torch.float16)
+    assert torch.equal(y, y_rm)
+
+
+@pytest.mark.parametrize("lr", [16, 32, 64])
+def test_gemm_packed_group32_lowrank_scatter(oracle, cuda, lr):
+    """Group-32 with a low-rank branch and a routed scatter: within the tolerance of the oracle, equal to the
+    row-major kernel, untouched canvas rows keep their bits."""
+    from pyraquant_amd import int8_exec as E
+
+    M, N, K, C = 500, 1280, 1280, 2000
+    a, w = _codes(M, N, K, lr, cuda)
+    g = torch.Generator().manual_seed(lr)
+    s_row = torch.rand(M, generator=g) * 0.05 + 1e-3
+    s_w = torch.rand(N, K // 32, generator=g) * 2e-4 + 1e-5
+    t = (torch.randn(M, lr, generator=g) * 0.5).to(torch.float16)
+    l2t = (torch.randn(N, lr, generator=g) * 0.02).to(torch.float16)
+    rows = torch.randperm(C, generator=g)[:M].to(torch.int32)
+    canvas = torch.randn(C, N, generator=g).to(torch.float16)
+    before = bits(canvas)
+    s_gn = s_w.t().contiguous().to(cuda)
+    out = canvas.to(cuda)
+    E.int8_gemm_packed(E.pack_k64(a), s_row.to(cuda), E.pack_k64(w), s_gn, None, M, N, K, torch.float16,
+                       t=t.to(cuda), l2t=l2t.to(cuda), out=out, out_row_idx=rows.to(cuda), group=32)
+    out_rm = canvas.to(cuda)
+    E._gemm(a, s_row.to(cuda), w, s_gn, 32, None, t.to(cuda), l2t.to(cuda), torch.float16, out_rm, rows.to(cuda))
+    assert torch.equal(out, out_rm)
+    got = bits(out)
+    r = rows.numpy()
+    keep = np.setdiff1d(np.arange(C), r)
+    assert np.array_equal(got[keep], before[keep])
+    part = oracle.gemm_group_i32(a.cpu().numpy(), w.cpu().numpy(), 32)
+    yo = oracle.epilogue_f32(part, s_row.numpy(), s_w.numpy(), None, bits(t), bits(l2t.t().contiguous()), 1)
+    mx, mean = rel_errors(oracle.to_f32(got[r], 1), yo)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
