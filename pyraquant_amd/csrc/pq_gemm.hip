@@ -152,6 +152,120 @@ struct Epilogue {
     }
   }
 
+  // ---- operands in LDS (run_lds) ----
+  // The first two ring stages past the end of K carry the epilogue operands instead of operand tiles (1 KB slots):
+  //   row buffer:    [s_row[m0 ..]] [out_row_idx[m0 ..]] [t rows m0 .., R 16-bit values each]
+  //   column buffer: [s_w[n0 ..]]   [bias[n0 ..]]        [l2t rows n0 .., R 16-bit values each]
+  // The t / l2t rows are packed back to back and cut into 64-byte lines that are swizzled like the operand tiles
+  // (16-byte chunk c of line L at slot c ^ swz(L % 16)), so the low-rank fragment reads are conflict free.
+  static constexpr int kR = 16 * RS;
+  __device__ __forceinline__ static int lr_off(int row, int rs, int kh) {
+    const int b = row * kR * 2 + rs * 32 + kh * 16;
+    const int line = b >> 6, ch = (b >> 4) & 3;
+    return 2048 + line * 64 + ((ch ^ k64_swz(line & 15)) << 4);
+  }
+  // Output staging of run_lds: 32 rows x 64 outputs (two weight tiles) per pass, rows padded by 16 bytes.
+  static constexpr int kPitchL = 128 + 16;
+  static constexpr int kStageBytesL = 32 * kPitchL;
+
+  // nloc / mloc: the wave's first column / row inside the workgroup block; nbase / mbase: the same, global.
+  template <typename AccT>
+  __device__ __forceinline__ void run_lds(const GemmArgs& p, AccT (&acc)[TI][TJ], int nloc, int mloc, int nbase,
+                                          int mbase, int lane, uint8_t* stage, const uint8_t* cbuf,
+                                          const uint8_t* rbuf) {
+    static_assert(MODE != kModeI32 && TI % 2 == 0, "run_lds: dequant modes, pairs of weight tiles");
+    const int khalf = lane >> 5;
+    const bool has_bias = p.bias != nullptr;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int ml = mloc + j * 32 + (lane & 31);
+      sr[j] = reinterpret_cast<const float*>(rbuf)[ml];
+      if constexpr (HAS_LR) {
+#pragma unroll
+        for (int rs = 0; rs < RS; ++rs) tv[j][rs] = *reinterpret_cast<const v4i*>(rbuf + lr_off(ml, rs, khalf));
+      }
+    }
+    if constexpr (MODE == kModeChannel) {
+      // see run(): explicit MFMA -> v_accvgpr_read distance
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const int* orows = reinterpret_cast<const int*>(rbuf + 1024);
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+#pragma unroll
+      for (int ih = 0; ih < TI / 2; ++ih) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+          const int i = 2 * ih + ii;
+          const int nl = nloc + 32 * i;
+          if constexpr (MODE == kModeChannel) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              sc[0][q] = *reinterpret_cast<const v4f*>(cbuf + (nl + 4 * khalf + 8 * q) * 4);
+          }
+          if (has_bias) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              bi[0][q] = *reinterpret_cast<const v4f*>(cbuf + 1024 + (nl + 4 * khalf + 8 * q) * 4);
+          }
+          if constexpr (HAS_LR) {
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs)
+              lb[0][rs] = *reinterpret_cast<const v4i*>(cbuf + lr_off(nl + (lane & 31), rs, khalf));
+          }
+          tile(acc[i][j], j, 0, has_bias, stage + (lane & 31) * kPitchL + (ii * 32 + 4 * khalf) * 2);
+        }
+        // staging -> global: 8 lanes x 16 bytes per 128-byte row piece, 8 rows per store instruction
+        const int lr_ = lane >> 3, lc = lane & 7;
+        const int n = nbase + ih * 64 + lc * 8;
+        const bool nvalid = n < p.N;
+#pragma unroll
+        for (int s0 = 0; s0 < 32; s0 += 8) {
+          const int row = s0 + lr_;
+          const int m = mbase + j * 32 + row;
+          const v4u v = *reinterpret_cast<const v4u*>(stage + row * kPitchL + lc * 16);
+          if (nvalid && m < p.M) {
+            const int64_t o = p.out_row_idx ? (int64_t)orows[mloc + j * 32 + row] : (int64_t)m;
+            *reinterpret_cast<v4u*>(static_cast<uint16_t*>(p.c) + o * p.ldc + n) = v;
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  // One 32 x 32 tile: dequant (+ low rank, + bias) in the reference's order, rounded to 16 bits and written to
+  // `dst` (this lane's row in the staging area, at its first output column): outputs 8 q + 4 (lane / 32) .. + 3.
+  template <typename AccV>
+  __device__ __forceinline__ void tile(const AccV& a, int j, int c, bool has_bias, uint8_t* dst) {
+    v16f y;
+    if constexpr (MODE == kModeChannel) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) y[r] = (float)acc_read(a[r]) * (sr[j] * sc[c][r >> 2][r & 3]);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) y[r] = a[r] * sr[j];
+    }
+    if constexpr (HAS_LR) {
+      // y += t[m, :] . l2t[n, :] (fp32 accumulation of the 16-bit operands, deploy/int8_exec.py:304-307)
+      v16f lr = v16f{};
+#pragma unroll
+      for (int rs = 0; rs < RS; ++rs) lr = lr_mfma<LRDT>(lb[c][rs], tv[j][rs], lr);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) y[r] = y[r] + lr[r];
+    }
+    if (has_bias) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) y[r] = y[r] + bi[c][r >> 2][r & 3];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *reinterpret_cast<v2u*>(dst + 16 * q) =
+          v2u{pack2<ODT>(y[4 * q + 0], y[4 * q + 1]), pack2<ODT>(y[4 * q + 2], y[4 * q + 3])};
+  }
+
   // Rows of the wave's output sub-tile (32 TJ rows of 32 TI outputs) staged in LDS by run(): 16-bit outputs,
   // rows padded by 16 bytes so that the column-wise fragment writes spread over the banks.
   static constexpr int kRowBytes = 64 * TI;
@@ -213,32 +327,8 @@ struct Epilogue {
         const int c = CB == 2 ? (i & 1) : 0;
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-          v16f y;
-          if constexpr (MODE == kModeChannel) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) y[r] = (float)acc_read(acc[i][j][r]) * (sr[j] * sc[c][r >> 2][r & 3]);
-          } else {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) y[r] = acc[i][j][r] * sr[j];
-          }
-          if constexpr (HAS_LR) {
-            // y += t[m, :] . l2t[n, :] (fp32 accumulation of the 16-bit operands, deploy/int8_exec.py:304-307)
-            v16f lr = v16f{};
-#pragma unroll
-            for (int rs = 0; rs < RS; ++rs) lr = lr_mfma<LRDT>(lb[c][rs], tv[j][rs], lr);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) y[r] = y[r] + lr[r];
-          }
-          if (has_bias) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) y[r] = y[r] + bi[c][r >> 2][r & 3];
-          }
           // fragment -> staging rows: row (32 j + lane % 32), outputs 32 i + 8 q + 4 (lane / 32) .. + 3
-          uint8_t* srow_j = stage + (j * 32 + (lane & 31)) * kPitch + (i * 32 + 4 * khalf) * 2;
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<v2u*>(srow_j + 16 * q) =
-                v2u{pack2<ODT>(y[4 * q + 0], y[4 * q + 1]), pack2<ODT>(y[4 * q + 2], y[4 * q + 3])};
+          tile(acc[i][j], j, c, has_bias, stage + (j * 32 + (lane & 31)) * kPitch + (i * 32 + 4 * khalf) * 2);
           __builtin_amdgcn_sched_barrier(0);   // keep one tile's epilogue live at a time
         }
       }
@@ -274,11 +364,14 @@ __device__ __forceinline__ int swz(int r) { return k64_swz(r); }
 template <int N>
 __device__ __forceinline__ void wait_dma() { wait_vmcnt<N>(); }
 
-template <int TI, int TJ, int NS, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
-__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(OCC, OCC)))
+// WMW waves along m (2 or 4) times 2 along n; OCC workgroups per CU.
+template <int TI, int TJ, int WMW, int NS, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
+__global__ __attribute__((amdgpu_flat_work_group_size(128 * WMW, 128 * WMW),
+                          amdgpu_waves_per_eu(OCC * WMW / 2, OCC * WMW / 2)))
 void gemm_dma_kernel(const GemmArgs p) {
   constexpr bool G32 = MODE == kModeGroup32;
-  constexpr int BN = 64 * TI, BM = 64 * TJ;
+  constexpr int NW = 2 * WMW;                 // waves per workgroup
+  constexpr int BN = 64 * TI, BM = 32 * TJ * WMW;
   constexpr int WB = BN * kBKd, AB = BM * kBKd;
   constexpr int SB = G32 ? 2 * BN * 4 : 0;    // group-32: the stage's two scale rows s_w[g, n0 .. n0 + BN)
   constexpr int STAGE = WB + AB;
@@ -286,9 +379,19 @@ void gemm_dma_kernel(const GemmArgs p) {
   // The DMA issued in iteration kt (stage kt + NS) then refills the slot of stage kt - 1, which every wave has
   // finished reading before the barrier of iteration kt, so the MFMA substeps read their scales straight from LDS.
   constexpr int SLOTS = NS + 1;
-  constexpr int DW = BN / 64, DA = BM / 64;   // 1 KB DMA instructions per wave and stage (W, A)
-  constexpr int DS = SB / 256 / 4;            // 256-byte (dword) DMA instructions per wave and stage (scales)
+  constexpr int DW = BN / 16 / NW, DA = BM / 16 / NW;   // 1 KB DMA instructions per wave and stage (W, A)
+  constexpr int DS = SB / 256 / NW;           // 256-byte (dword) DMA instructions per wave and stage (scales)
+  static_assert(DW * 16 * NW == BN && DA * 16 * NW == BM && DS * 256 * NW == SB, "DMA split over the waves");
   constexpr int DPW = DW + DA + DS;
+  // Epilogue operands through the ring (run_lds): the row and column slots must fit one stage each and the
+  // operand DMA slots of one stage, and the output staging the remaining NS - 2 buffers.
+  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT, OCC * WMW == 2 ? 2 : 1>;
+  constexpr int kLrBytes = LRS * 16 * 2;                       // one low-rank row
+  constexpr int kRowSlots = 2 + BM * kLrBytes / 1024, kColSlots = 2 + BN * kLrBytes / 1024;
+  constexpr bool ELDS = MODE != kModeI32 && TI % 2 == 0 && NS >= 3 && BN <= 256 && BM <= 256 &&
+                        kRowSlots * 1024 <= WB + AB && kColSlots * 1024 <= WB + AB &&
+                        kRowSlots <= NW * (DW + DA) && kColSlots <= NW * (DW + DA) &&
+                        (NS - 2) * ((WB + AB) / Epi::kStageBytesL) >= NW;
   constexpr int NF = TI + TJ;                 // fragments per substep
   constexpr int kRest = TI * TJ - NF;         // MFMAs of a substep beyond the NF that carry a fragment read
   constexpr int kVPer = kRest > 0 ? (DPW + kRest - 1) / (kRest > 0 ? kRest : 1) : 0;   // DMA per such MFMA
@@ -373,12 +476,63 @@ void gemm_dma_kernel(const GemmArgs p) {
     }
   };
 
+  // DMA of a stage s >= KT (no operand data left). With ELDS, stage KT brings the row operands of the epilogue and
+  // stage KT + 1 the column operands (slot q: the WG's 16-byte DMA instruction wave * (DW + DA) + i; slots past
+  // the last one repeat it, which rewrites the same bytes); later stages load nothing. Every stage issues DPW
+  // instructions per wave either way, which keeps the vmcnt arithmetic of the ring valid.
+  auto dma_tail = [&](int buf, int st) {
+    if constexpr (ELDS) {
+      if (st == KT || st == KT + 1) {
+        uint8_t* sb = smem + buf * STAGE;
+        const bool rows = st == KT;
+        const int nsl = rows ? kRowSlots : kColSlots;
+        const int rows_x = rows ? rows_a : rows_w;
+        const float* sv = rows ? p.s_row + m0 : p.s_w + n0;
+        const void* iv = rows ? (const void*)p.out_row_idx : (const void*)p.bias;
+        const int ioff = rows ? m0 : n0;
+        const __amdgpu_buffer_rsrc_t rs_v = __builtin_amdgcn_make_buffer_rsrc((void*)sv, (short)0, rows_x * 4,
+                                                                             kBufferWord3);
+        const __amdgpu_buffer_rsrc_t rs_i = __builtin_amdgcn_make_buffer_rsrc(
+            iv ? (void*)(static_cast<const int*>(iv) + ioff) : (void*)p.s_w, (short)0, iv ? rows_x * 4 : 0,
+            kBufferWord3);
+        // low-rank rows: t (row stride ldt) or l2t (row stride R)
+        const int64_t lrs = rows ? p.ldt : (int64_t)LRS * 16;
+        const uint16_t* lp = rows ? p.t + (int64_t)m0 * p.ldt : p.l2t + (int64_t)n0 * LRS * 16;
+        const int lrec = LRS ? (int)((rows_x - 1) * lrs * 2 + kLrBytes) : 0;
+        const __amdgpu_buffer_rsrc_t rs_l = __builtin_amdgcn_make_buffer_rsrc(
+            LRS ? (void*)lp : (void*)p.s_w, (short)0, lrec, kBufferWord3);
+#pragma unroll
+        for (int i = 0; i < DW + DA; ++i) {
+          const int q = min(wave * (DW + DA) + i, nsl - 1);
+          int vo = lane * 16;
+          __amdgpu_buffer_rsrc_t rs = q == 0 ? rs_v : rs_i;
+          if (q >= 2) {
+            // packed byte of slot lane: line L = 16 (q - 2) + lane / 4, stored chunk (lane % 4) ^ swz(L % 16)
+            const int pb = ((q - 2) * 16 + (lane >> 2)) * 64 + (((lane & 3) ^ swz(lane >> 2)) << 4);
+            const int row = pb / kLrBytes, cb = pb % kLrBytes;
+            vo = (int)(row * lrs * 2) + cb;
+            rs = rs_l;
+          }
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(sb + q * 1024), 16, vo, 0, 0, 0);
+        }
+        if constexpr (G32) {
+#pragma unroll
+          for (int i = 0; i < DS; ++i)   // scale slots: out of range, as in dma()
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_s, (lds_void_t*)(sscale + (st % SLOTS) * SB + (wave * DS + i) * 256),
+                                                     4, vs + kOOB, 0, 0, 0);
+        }
+        return;
+      }
+    }
+    dma(buf, st);
+  };
+
   // MFMA operand reads: lane reads tile row (lane % 32) of each 32-row fragment, K chunk 2 s + lane / 32 of
   // substep s. Fragment rows are 32-aligned, so swz(row) = swz(lane % 16).
   const int sw = swz(lane & 15);
   const int kh = lane >> 5;
   const int fw_off = (wn * (BN / 2) + (lane & 31)) * kBKd;
-  const int fa_off = WB + (wm * (BM / 2) + (lane & 31)) * kBKd;
+  const int fa_off = WB + (wm * (BM / WMW) + (lane & 31)) * kBKd;
 
   using acc_t = typename std::conditional<G32, v16f, v16i>::type;
   acc_t acc[TI][TJ];
@@ -455,13 +609,14 @@ void gemm_dma_kernel(const GemmArgs p) {
   // must have landed at the barrier that ends iteration s - 1, NS - 1 iterations later; in between, the DMAs of
   // NS - 2 younger stages may still be in flight, hence vmcnt((NS - 2) * DPW).
 #pragma unroll
-  for (int st = 0; st < NS; ++st) dma(st, st);
+  for (int st = 0; st < NS; ++st) {
+    if (st < KT) dma(st, st);
+    else dma_tail(st, st);
+  }
   wait_dma<(NS - 1) * DPW>();
   __syncthreads();
   rd(f0, 0, 0);
-  int b = 0;
-  for (int kt = 0; kt < KT - 1; ++kt) {
-    const int bn = b + 1 == NS ? 0 : b + 1;
+  auto iter = [&](int kt, int b, int bn, auto tail) {
     rd(f1, b, 1);
     mm(f0, kt, 0);
     interleave(no_dma{});
@@ -469,23 +624,43 @@ void gemm_dma_kernel(const GemmArgs p) {
     __syncthreads();              // every wave's has, and every wave is done reading buffer b
     __builtin_amdgcn_sched_barrier(0);
     rd(f0, bn, 0);
-    dma(b, kt + NS);
+    if constexpr (decltype(tail)::value) dma_tail(b, kt + NS);
+    else dma(b, kt + NS);
     mm(f1, kt, 1);
     interleave(with_dma{});
+  };
+  int b = 0;
+  int kt = 0;
+  for (; kt < KT - NS; ++kt) {      // stages kt + NS < KT: operand DMA
+    const int bn = b + 1 == NS ? 0 : b + 1;
+    iter(kt, b, bn, no_dma{});
+    b = bn;
+  }
+  for (; kt < KT - 1; ++kt) {       // the last NS - 1 iterations: epilogue operands (dma_tail)
+    const int bn = b + 1 == NS ? 0 : b + 1;
+    iter(kt, b, bn, with_dma{});
     b = bn;
   }
   // last stage: the epilogue's operands are fetched under its MFMAs
-  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT, OCC == 1 ? 2 : 1>;
   Epi epi;
-  const int nbase = n0 + wn * (BN / 2), mbase = m0 + wm * (BM / 2);
-  epi.prefetch_rows(p, mbase, lane);
+  const int nbase = n0 + wn * (BN / 2), mbase = m0 + wm * (BM / WMW);
+  if constexpr (!ELDS) epi.prefetch_rows(p, mbase, lane);
   rd(f1, b, 1);
   mm(f0, KT - 1, 0);
   mm(f1, KT - 1, 1);
-  static_assert(4 * Epi::kStageBytes <= NS * STAGE, "output staging must fit the LDS ring");
-  wait_dma<0>();     // the out-of-range DMAs of the last iterations may still target the ring
+  wait_dma<0>();     // the epilogue operands, and the out-of-range DMAs of the last iterations, have landed
   __syncthreads();   // every wave is done reading the ring: it becomes the output staging area
-  epi.run(p, acc, nbase, mbase, lane, smem + wave * Epi::kStageBytes);
+  if constexpr (ELDS) {
+    // buffers of stages KT (rows) and KT + 1 (columns) hold the operands; staging in the NS - 2 others
+    constexpr int kSpb = STAGE / Epi::kStageBytesL;
+    const int k = wave / kSpb;
+    uint8_t* stage = smem + ((KT + 2 + k) % NS) * STAGE + (wave % kSpb) * Epi::kStageBytesL;
+    epi.run_lds(p, acc, wn * (BN / 2), wm * (BM / WMW), nbase, mbase, lane, stage, smem + ((KT + 1) % NS) * STAGE,
+                smem + (KT % NS) * STAGE);
+  } else {
+    static_assert(ELDS || NW * Epi::kStageBytes <= NS * STAGE, "output staging must fit the LDS ring");
+    epi.run(p, acc, nbase, mbase, lane, smem + wave * Epi::kStageBytes);
+  }
 }
 
 // ---- launchers ---------------------------------------------------------------------------------------------
@@ -500,20 +675,21 @@ int grid_of(GemmArgs& a, int BM, int BN, dim3& grid) {
 
 // Ring depth: as many 64-byte K stages as fit this workgroup's share of the 160 KB LDS (5 x 32 KB for 256 x 256
 // blocks at one workgroup per CU, 3 x 24 KB for 256 x 128 blocks at two per CU), at most 8.
-template <int TI, int TJ, int OCC, int MODE>
+template <int TI, int TJ, int WMW, int OCC, int MODE>
 constexpr int ring_stages() {
-  constexpr int stage = (64 * TI + 64 * TJ) * kBKd, sb = MODE == kModeGroup32 ? 2 * 64 * TI * 4 : 0;
+  constexpr int stage = (64 * TI + 32 * TJ * WMW) * kBKd, sb = MODE == kModeGroup32 ? 2 * 64 * TI * 4 : 0;
   constexpr int ns = (160 * 1024 / OCC - sb) / (stage + sb);   // NS operand stages + NS + 1 scale slots
   return ns < 8 ? ns : 8;
 }
 
-template <int TI, int TJ, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
+template <int TI, int TJ, int WMW, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 int launch_dma(GemmArgs& a, hipStream_t stream) {
-  constexpr int NS = ring_stages<TI, TJ, OCC, MODE>();
+  constexpr int NS = ring_stages<TI, TJ, WMW, OCC, MODE>();
   dim3 grid;
-  const int st = grid_of(a, 64 * TJ, 64 * TI, grid);
+  const int st = grid_of(a, 32 * TJ * WMW, 64 * TI, grid);
   if (st != PQ_OK) return st;
-  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, NS, OCC, PACKED, MODE, LRS, LRDT, ODT>), grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, WMW, NS, OCC, PACKED, MODE, LRS, LRDT, ODT>), grid, dim3(128 * WMW), 0,
+                     stream, a);
   return check_launch("int8_gemm");
 }
 
@@ -529,10 +705,10 @@ template <bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
   if constexpr (MODE == kModeGroup32) {
     // fp32 accumulators live in VGPRs (the VALU rescales them every group): 128 x 128 blocks, two per CU
-    return launch_dma<2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
   } else {
-    if (big_tiles(a)) return launch_dma<4, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
-    return launch_dma<2, 2, 1, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    if (big_tiles(a)) return launch_dma<4, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    return launch_dma<2, 2, 2, 1, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
   }
 }
 
@@ -624,8 +800,8 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
   args.a = a; args.w = w; args.c = c;
   args.lda = lda; args.ldw = ldw; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
-  if (big_tiles(args)) return launch_dma<4, 2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
-  return launch_dma<2, 2, 1, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+  if (big_tiles(args)) return launch_dma<4, 2, 2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+  return launch_dma<2, 2, 2, 1, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
 }
 
 extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
@@ -649,8 +825,8 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
     if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 16)
       return set_error(PQ_EALIGN, "pq_int8_gemm_packed: int32 c must be 16-byte aligned with ldc %% 4 == 0");
     args.ldc = ldc;
-    if (big_tiles(args)) return launch_dma<4, 2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
-    return launch_dma<2, 2, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+    if (big_tiles(args)) return launch_dma<4, 2, 2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+    return launch_dma<2, 2, 2, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
   }
   if (!s_row || !s_w) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null s_row / s_w");
   if (group != 0 && group != 32)
