@@ -2,8 +2,9 @@
 """Benchmark of the INT8 deployment hot path on one MI355X: one Int8Linear forward per step at the FLUX 4K MLP
 up-projection (config c1: M=65536 tokens, K=3072, N=12288, rank-32 low-rank branch, bias, bf16 in/out).
 
-A step is the whole layer on inputs already resident in HBM, as Int8Linear.forward runs it: low-rank
-down-projection (t = x @ L1), per-token quantizer writing packed K64 codes, fused INT8 GEMM over packed operands
+A step is the whole layer on inputs already resident in HBM, as Int8Linear.forward runs it: per-token quantizer
+writing packed K64 codes and the low-rank down-projection (t = x @ L1) in one pass over x, fused INT8 GEMM over
+packed operands
 + dequant + low-rank up + bias epilogue (group-32 layers: per-group rescale in the GEMM's main loop). `value` = 2*M*N*K / step time (INT8 TOPS
 of the whole layer). `roofline` prices the dominant kernel (the fused GEMM) against the dense INT8 MFMA peak
 (5.0 POP/s) from HIP events recorded around every GEMM launch of the timed steps, on the stream it runs on.
@@ -81,9 +82,18 @@ def main() -> int:
             return e
 
         e0 = mark()
-        t = E.lowrank_down(x, q.lr_At, rows) if q.lr_At is not None else None
-        e1 = mark()
-        if q.weight_packed is not None:
+        fused = q.weight_packed is not None and q.lr_At is not None
+        if fused:   # quantizer + low-rank down-projection in one pass over x, as Int8Linear.forward runs it
+            e1 = e0
+            xq, sx, t = E.quant_rows_lowrank(x, q.lr_At, rows)
+            e2 = mark()
+        else:
+            t = E.lowrank_down(x, q.lr_At, rows) if q.lr_At is not None else None
+            e1 = mark()
+        if fused:
+            E.int8_gemm_packed(xq, sx, q.weight_packed, q._scale_k(), q.bias, M, cfg.N, cfg.K, cfg.dtype, t=t,
+                               l2t=q.lr_Bt, out=out, out_row_idx=rows, group=q.group_size)
+        elif q.weight_packed is not None:
             xq, sx = E.quant_rows_packed(x, rows)
             e2 = mark()
             E.int8_gemm_packed(xq, sx, q.weight_packed, q._scale_k(), q.bias, M, cfg.N, cfg.K, cfg.dtype, t=t,
@@ -94,7 +104,7 @@ def main() -> int:
             E._gemm(xq, sx, q.weight_int8, q._scale_k(), q.group_size, q.bias, t, q.lr_Bt, cfg.dtype, out, rows)
         e3 = mark()
         if record:
-            if t is not None:
+            if t is not None and not fused:
                 ev["down"].append((e0, e1))
             ev["quant"].append((e1, e2))
             ev["gemm"].append((e2, e3))
@@ -118,7 +128,11 @@ def main() -> int:
     gemm_ms = avg_ms("gemm")
     gemm_tops = ops / (gemm_ms * 1e-3) / 1e12
     quant_ms = avg_ms("quant")
+    fused = q.weight_packed is not None and q.lr_At is not None
+    # quantizer bytes: bf16 read + int8 codes + fp32 scale (+ index read); the fused pass also writes t
     quant_bytes = 3.0 * M * cfg.K + 4.0 * M + (4.0 * M if rows is not None else 0.0)
+    if fused:
+        quant_bytes += 2.0 * M * cfg.lowrank
     quant_gbs = quant_bytes / (quant_ms * 1e-3) / 1e9
     down_ms = avg_ms("down")
 
@@ -156,8 +170,9 @@ def main() -> int:
             "M": M, "K": cfg.K, "N": cfg.N,
             "us_per_layer": round(ms_step * 1e3, 1),
             "pct_int8_peak_layer": round(100.0 * value / INT8_PEAK_TOPS, 2),
-            "kernels_us": {"lowrank_down": round(down_ms * 1e3, 1), "quant_rows": round(quant_ms * 1e3, 1),
-                           "int8_gemm": round(gemm_ms * 1e3, 1)},
+            "kernels_us": ({"quant_rows_lowrank": round(quant_ms * 1e3, 1)} if fused else
+                           {"lowrank_down": round(down_ms * 1e3, 1), "quant_rows": round(quant_ms * 1e3, 1)}) |
+                          {"int8_gemm": round(gemm_ms * 1e3, 1)},
             "quant_rows_GBps": round(quant_gbs, 1),
             "quant_rows_frac_hbm": round(quant_gbs / HBM_PEAK_GBS, 4),
         },

@@ -135,6 +135,19 @@ int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
                      int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 /*
+ * Per-token quantizer (packed K64 codes, as pq_quant_rows_packed) and the rank-R low-rank down-projection
+ * t = x[rows] @ L1 (as pq_lowrank_down) from one pass over x: the two steps of Int8Linear.forward that read x,
+ * `t = x2.to(lr_A.dtype) @ lr_A` and `quant_rows(x2)` (deploy/int8_exec.py:390-391). qp / s are bit-identical to
+ * pq_quant_rows_packed; t is the fp32-accumulated product rounded to the 16-bit type, as pq_lowrank_down (the
+ * accumulation order differs, so the last bit of t may differ from it). x is read from HBM once when R == 32,
+ * K is one of 1024, 1280, 2048, 2560, 3072, rows are 16-byte aligned (ldx % 8 == 0) and every x byte offset fits
+ * 30 bits; other shapes run the two kernels. l1t [R, K] contiguous, same dtype as x; t [M, R] with row stride ldt.
+ */
+int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
+                          const int32_t* row_idx, const void* l1t, int64_t R, int8_t* qp, float* s, void* t,
+                          int64_t ldt, hipStream_t stream);
+
+/*
  * Fused INT8 GEMM over packed K64 operands (ap: activation codes [M, K], wp: weights [N, K], both in the packed
  * K64 layout). Same math, epilogue, scatter and requirements as pq_int8_gemm (group 0: s_w [N]; group 32:
  * s_w [K/32, N] group-major); with out_dtype == PQ_I32, c receives the raw int32 accumulator (s_row, s_w, group,

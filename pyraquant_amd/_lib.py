@@ -30,6 +30,7 @@ EXPORTS = (
     "pq_int8_gemm_packed",
     "pq_pack_k64",
     "pq_quant_rows_packed",
+    "pq_quant_rows_lowrank",
     "pq_dequant_epilogue",
 )
 
@@ -51,6 +52,7 @@ _SIGNATURES = {
                             ctypes.c_int),
     "pq_pack_k64": ([_p, _i64, _i64, _i64, _p, _p], ctypes.c_int),
     "pq_quant_rows_packed": ([_p, _i32, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
+    "pq_quant_rows_lowrank": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p], ctypes.c_int),
     "pq_dequant_epilogue": ([_p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p], ctypes.c_int),
 }
 

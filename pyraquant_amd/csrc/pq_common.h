@@ -27,6 +27,7 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 // ---- LDS-DMA helpers ---------------------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int kBufferWord3 = 0x00020000;   // gfx9 buffer descriptor word 3 (raw, 32-bit data format)
+constexpr int kOOB = 0x40000000;           // buffer offset beyond every operand's num_records (loads nothing)
 
 // s_waitcnt vmcnt(N) (expcnt / lgkmcnt left at their maxima). The compiler does not count LDS-DMA loads as
 // LDS writes before a barrier, so every hand-over of a DMA-filled LDS stage waits for them explicitly.

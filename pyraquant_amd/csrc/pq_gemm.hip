@@ -37,7 +37,6 @@ namespace pq {
 namespace {
 
 constexpr int kGroupM = 8;                 // m-tiles per raster group
-constexpr int kOOB = 0x40000000;           // buffer offset beyond every operand's num_records (loads nothing)
 
 struct GemmArgs {
   const int8_t* a;
@@ -509,7 +508,8 @@ void gemm_dma_kernel(const GemmArgs p) {
           if (q >= 2) {
             // packed byte of slot lane: line L = 16 (q - 2) + lane / 4, stored chunk (lane % 4) ^ swz(L % 16)
             const int pb = ((q - 2) * 16 + (lane >> 2)) * 64 + (((lane & 3) ^ swz(lane >> 2)) << 4);
-            const int row = pb / kLrBytes, cb = pb % kLrBytes;
+            constexpr int kLb = kLrBytes > 0 ? kLrBytes : 1;   // (no low rank: never reached)
+            const int row = pb / kLb, cb = pb % kLb;
             vo = (int)(row * lrs * 2) + cb;
             rs = rs_l;
           }

@@ -15,6 +15,7 @@
 // element in 10^4) redo that element with the correctly rounded division.
 #include "pq_common.h"
 
+#include <algorithm>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -392,6 +393,140 @@ __global__ __launch_bounds__(256) void lowrank_down_dma_kernel(
   }
 }
 
+// ---- fused quantizer + low-rank down-projection (one read of x) ----------------------------------------------
+// pq_quant_rows_packed and pq_lowrank_down (R = 32) in one pass: deploy/int8_exec.py:390-391 computes
+// t = x @ lr_A and quant_rows(x) from the same x, and both need every element of a row.
+// One workgroup of 4 waves per CU, persistent over batches of 16 rows. A batch is brought into LDS by LDS-DMA in
+// 1 KB row-contiguous pieces (the DRAM-friendly pattern of the row-per-wave quantizer), then every wave reads its
+// K quarter [w K / 4, (w + 1) K / 4) of the 16 rows into registers (lane: row l % 16, K group l / 16), the DMA of the
+// next batch is issued into the freed buffer, and the wave works from registers:
+//   absmax over the quarter -> LDS -> the row scale (the same IEEE steps as quant_rows_vec_kernel); codes from the
+//   registers (quant_chunk), each wave storing whole 16-row x 64-byte packed K64 blocks;
+//   t partial = the quarter of x . l1t by v_mfma_f32_16x16x32, whose l1t slice stays in registers for the whole
+//   kernel -> LDS -> t = ((p0 + p1) + p2) + p3 in fp32, rounded to the 16-bit type.
+// K assignment inside the 64-wide K block c of a quarter (MFMA steps 2c and 2c + 1): lane group g covers
+// K [64 c + 16 g, +16), 8 values per step. Both MFMA operands use it, so each step contracts 32 distinct K; the
+// 16 codes a lane produces per block are chunk g of its row's 64-byte segment.
+template <int DT, int NC>   // NC: 64-wide K blocks per wave, K = 256 NC
+__global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int64_t M, const int32_t* __restrict__ row_idx,
+    const uint16_t* __restrict__ l1t, int8_t* __restrict__ qp, float* __restrict__ s, uint16_t* __restrict__ t,
+    int64_t ldt, int nbatch) {
+  constexpr int K = 256 * NC, R = 32, NS = 2 * NC;
+  constexpr int CHUNKS = (2 * K + 1023) / 1024;      // 1 KB DMA pieces per row
+  constexpr int PITCH = CHUNKS * 1024 + 64;          // LDS row pitch (+64 bytes: rows start 16 banks apart)
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[16 * PITCH];
+  __shared__ uint32_t amax_l[4][16];
+  __shared__ __attribute__((aligned(16))) float red[4][16][R];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int k0 = wave * (K / 4);
+  const int G = gridDim.x;
+  const __amdgpu_buffer_rsrc_t rs_x =
+      __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, (int)(x_rows * ldx * 2), kBufferWord3);
+
+  // l1t fragments of this wave's quarter: lf[h][2 c + e] = l1t[16 h + r][k0 + 64 c + 16 g + 8 e .. + 8]
+  v4u lf[2][NS];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+      lf[h][i] = *reinterpret_cast<const v4u*>(l1t + (int64_t)(16 * h + r) * K + k0 + 64 * (i >> 1) + 16 * g +
+                                               8 * (i & 1));
+
+  // DMA of batch b: wave w copies rows 4 w .. 4 w + 3, CHUNKS pieces each (rows past M: out of range, zeros).
+  // Source rows come from uniform (scalar) reads of the gather list, so no vector load joins the vmcnt queue.
+  auto dma = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t m = (int64_t)b * 16 + wave * 4 + j;
+      int off = kOOB;
+      if (m < M) off = (int)((row_idx ? (int64_t)row_idx[m] : m) * ldx * 2);
+#pragma unroll
+      for (int c = 0; c < CHUNKS; ++c)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (lds_void_t*)(xs + (wave * 4 + j) * PITCH + c * 1024), 16,
+                                                 off + c * 1024 + lane * 16, 0, 0, 0);
+    }
+  };
+
+  v4u xv[NS];
+  const uint8_t* xrow = xs + r * PITCH + 2 * (k0 + 16 * g);
+  int b = blockIdx.x;
+  dma(b);
+  for (; b < nbatch; b += G) {
+    // The DMA of batch b was followed only by the NC unconditional code stores of the previous batch (and maybe
+    // the scale and t stores): vmcnt <= NC leaves nothing older than those in flight.
+    wait_vmcnt<NC>();
+    __syncthreads();   // every wave's DMA of batch b has landed
+#pragma unroll
+    for (int i = 0; i < NS; ++i) xv[i] = *reinterpret_cast<const v4u*>(xrow + 128 * (i >> 1) + 16 * (i & 1));
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS reads are done
+    __syncthreads();                      // every wave's are: the buffer takes the next batch
+    dma(b + G < nbatch ? b + G : nbatch);
+    __builtin_amdgcn_sched_barrier(0);   // the stores below stay behind the DMA in the vmcnt queue
+
+    const int64_t m = (int64_t)b * 16 + r;
+    // absmax: magnitude bits, packed u16 max, then the 4 lanes of the row, then the 4 quarters
+    us2 mx2 = {0, 0};
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, xv[i].x & 0x7fff7fffu));
+      mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, xv[i].y & 0x7fff7fffu));
+      mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, xv[i].z & 0x7fff7fffu));
+      mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, xv[i].w & 0x7fff7fffu));
+    }
+    uint32_t mx = mx2.x > mx2.y ? mx2.x : mx2.y;
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_xor((int)mx, off, 64);
+      mx = mx > o ? mx : o;
+    }
+    if (g == 0) amax_l[wave][r] = mx;
+    // low rank: partial t over the quarter (independent of the scale)
+    v4f acc[2] = {v4f{}, v4f{}};
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (DT == PQ_BF16)
+          acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, lf[h][i]),
+                                                          __builtin_bit_cast(v8bf, xv[i]), acc[h], 0, 0, 0);
+        else
+          acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, lf[h][i]),
+                                                         __builtin_bit_cast(v8h, xv[i]), acc[h], 0, 0, 0);
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();   // amax_l complete (LDS only: the DMA of the next batch stays in flight)
+    uint32_t am = amax_l[0][r];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) am = am > amax_l[w][r] ? am : amax_l[w][r];
+    const float a = fmaxf(lo16_to_f32<DT>(am), 1e-8f);
+    const float sc = __fdiv_rn(a, 127.0f);
+    const float rc = __fdiv_rn(1.0f, sc);
+    // codes: block c of the quarter, chunk g of row m (padding rows past M quantize zeros to zero codes)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const v2u lo = quant_chunk<DT>(xv[2 * c], sc, rc);
+      const v2u hi = quant_chunk<DT>(xv[2 * c + 1], sc, rc);
+      *reinterpret_cast<v4u*>(qp + k64_offset(m, k0 + 64 * c + 16 * g, K / 64)) = v4u{lo.x, lo.y, hi.x, hi.y};
+    }
+    if (wave == 0 && g == 0 && m < M) s[m] = sc;
+    // D[rr][m]: lane holds m = r and rr = 16 h + 4 g + (0..3)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) *reinterpret_cast<v4f*>(&red[wave][r][16 * h + 4 * g]) = acc[h];
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();   // red complete
+    {
+      const int mr = tid >> 4, rr = (tid & 15) * 2;
+      const int64_t mo = (int64_t)b * 16 + mr;
+      const float v0 = ((red[0][mr][rr] + red[1][mr][rr]) + red[2][mr][rr]) + red[3][mr][rr];
+      const float v1 = ((red[0][mr][rr + 1] + red[1][mr][rr + 1]) + red[2][mr][rr + 1]) + red[3][mr][rr + 1];
+      if (mo < M) *reinterpret_cast<uint32_t*>(t + mo * ldt + rr) = pack2<DT>(v0, v1);
+    }
+  }
+}
+
 // ---- dequant epilogue over a materialised int32 accumulator ----------------------------------------------
 template <int DT>
 __global__ __launch_bounds__(256) void dequant_epilogue_kernel(
@@ -509,6 +644,43 @@ extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t 
   PQ_LRCASE(PQ_F16, 1) PQ_LRCASE(PQ_F16, 2) PQ_LRCASE(PQ_F16, 3) PQ_LRCASE(PQ_F16, 4)
 #undef PQ_LRCASE
   return set_error(PQ_ESHAPE, "pq_lowrank_down: unsupported rank");
+}
+
+// Fused per-token quantizer (packed K64 codes) + rank-32 low-rank down-projection: the results of
+// pq_quant_rows_packed and pq_lowrank_down on the same x, with x read once where the fused kernel applies
+// (R == 32, K in {1024, 1280, 2048, 2560, 3072}, 16-byte aligned rows, 32-bit x offsets); otherwise the two.
+extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+                                     int64_t x_rows, const int32_t* row_idx, const void* l1t, int64_t R, int8_t* qp,
+                                     float* s, void* t, int64_t ldt, hipStream_t stream) {
+  if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_rows_lowrank: bad shape M=%lld K=%lld", (long long)M, (long long)K);
+  if (M == 0) return PQ_OK;
+  if (!x || !qp || !s || !l1t || !t) return set_error(PQ_EINVAL, "pq_quant_rows_lowrank: null pointer");
+  const int nc = (int)(K / 256);
+  const bool fused = R == 32 && K % 256 == 0 && (nc == 4 || nc == 5 || nc == 8 || nc == 10 || nc == 12) &&
+                     ldx >= K && ldx % 8 == 0 && ldt >= R && ldt % 2 == 0 && x_rows >= 1 &&
+                     (row_idx || x_rows >= M) && x_rows * ldx * 2 + 2 * K <= 0x3fffffffLL &&
+                     (uintptr_t)x % 16 == 0 && (uintptr_t)l1t % 16 == 0 && (uintptr_t)t % 4 == 0 &&
+                     (uintptr_t)qp % 16 == 0 && (x_dtype == PQ_BF16 || x_dtype == PQ_F16);
+  if (!fused) {
+    const int st = pq_quant_rows_packed(x, x_dtype, M, K, ldx, row_idx, qp, s, stream);
+    if (st != PQ_OK) return st;
+    return pq_lowrank_down(x, x_dtype, M, K, ldx, x_rows, row_idx, l1t, R, t, ldt, stream);
+  }
+  const int nbatch = (int)((M + 15) / 16);
+  const dim3 block(256), grid((unsigned)std::min(nbatch, 256));
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  const uint16_t* lp = static_cast<const uint16_t*>(l1t);
+  uint16_t* tp = static_cast<uint16_t*>(t);
+#define PQ_QLCASE(D, NC)                                                                                     \
+  if (x_dtype == D && nc == NC) {                                                                           \
+    hipLaunchKernelGGL((quant_lowrank_kernel<D, NC>), grid, block, 0, stream, xp, ldx, x_rows, M, row_idx, lp, \
+                       qp, s, tp, ldt, nbatch);                                                             \
+    return check_launch("quant_rows_lowrank");                                                              \
+  }
+  PQ_QLCASE(PQ_BF16, 4) PQ_QLCASE(PQ_BF16, 5) PQ_QLCASE(PQ_BF16, 8) PQ_QLCASE(PQ_BF16, 10) PQ_QLCASE(PQ_BF16, 12)
+  PQ_QLCASE(PQ_F16, 4) PQ_QLCASE(PQ_F16, 5) PQ_QLCASE(PQ_F16, 8) PQ_QLCASE(PQ_F16, 10) PQ_QLCASE(PQ_F16, 12)
+#undef PQ_QLCASE
+  return set_error(PQ_ESHAPE, "pq_quant_rows_lowrank: unsupported shape");
 }
 
 extern "C" int pq_dequant_epilogue(const int32_t* acc, const float* s_row, const float* s_col,

@@ -228,6 +228,30 @@ def quant_rows_packed(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) 
     return q, s
 
 
+def quant_rows_lowrank(x2: torch.Tensor, lr_At: torch.Tensor,
+                       row_idx: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """quant_rows_packed(x2, row_idx) and lowrank_down(x2, lr_At, row_idx) from one pass over x2
+    (pq_quant_rows_lowrank; deploy/int8_exec.py:390-391). Returns (packed codes, scales, t)."""
+    assert x2.dim() == 2 and x2.is_cuda and lr_At.is_cuda
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    assert lr_At.dtype == x2.dtype, "x2 and lr_A must share a dtype (cast x2 first, as the reference does)"
+    rows, K = x2.shape
+    assert K % 64 == 0, K
+    assert lr_At.is_contiguous() and lr_At.shape[1] == K, "lr_At must be [R, K] contiguous"
+    R = lr_At.shape[0]
+    ri = _row_index(row_idx, x2.device)
+    M = rows if ri is None else ri.shape[0]
+    q = torch.empty((packed_rows(M) * K,), dtype=torch.int8, device=x2.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x2.device)
+    t = torch.empty((M, R), dtype=x2.dtype, device=x2.device)
+    L = _lib.load()
+    _lib.check(L.pq_quant_rows_lowrank(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), rows, _lib.ptr(ri),
+                                       _lib.ptr(lr_At), R, _lib.ptr(q), _lib.ptr(s), _lib.ptr(t), R,
+                                       _lib.stream_of(x2.device)), "quant_rows_lowrank")
+    return q, s, t
+
+
 def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor, w_scale: torch.Tensor,
                      bias: Optional[torch.Tensor], M: int, N: int, K: int, out_dtype: torch.dtype, *,
                      t: Optional[torch.Tensor] = None, l2t: Optional[torch.Tensor] = None,
@@ -383,13 +407,18 @@ class Int8Linear(nn.Module):
         if x2.stride(1) != 1:
             x2 = x2.contiguous()
         t = None
-        if self.lr_A is not None:
+        fused = self.weight_packed is not None and self.lr_A is not None and x2.dtype == self.lr_A.dtype
+        if fused:
+            # quantizer and low-rank down-projection from one pass over x (deploy/int8_exec.py:390-391)
+            xq, sx, t = quant_rows_lowrank(x2, self.lr_At, row_idx)
+        elif self.lr_A is not None:
             xl = x2 if x2.dtype == self.lr_A.dtype else x2.to(self.lr_A.dtype)
             t = lowrank_down(xl, self.lr_At, row_idx)
             if t.dtype != x2.dtype:
                 t = t.to(x2.dtype)
         if self.weight_packed is not None:
-            xq, sx = quant_rows_packed(x2, row_idx)
+            if not fused:
+                xq, sx = quant_rows_packed(x2, row_idx)
             y = int8_gemm_packed(xq, sx, self.weight_packed, self._scale_k(), self.bias, sx.shape[0],
                                  self.out_features, self.in_features, x2.dtype, t=t, l2t=self._lr_bt(x2.dtype),
                                  out=out, out_row_idx=out_row_idx, group=self.group_size)

@@ -1,0 +1,104 @@
+"""GPU parity of pq_quant_rows_lowrank, the quantizer and the rank-32 low-rank down-projection from one pass over x
+(deploy/int8_exec.py:390-391):
+* packed codes and scales bit-identical to pq_quant_rows_packed on the same rows (which the quantizer tests pin
+  against the oracle);
+* t within bf16 rounding of the float64 product and within the build's tolerance of the oracle's fp32 result;
+* shapes the fused kernel does not take (K outside its list, R != 32) give exactly what the two separate entry
+  points give.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import MAX_REL, MEAN_REL, bits, dcode, rel_errors
+
+pytestmark = pytest.mark.gpu
+
+
+def _l1(K, R, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(K, R, generator=g) * 0.02).to(dtype)
+
+
+def _check_t(oracle, t, x_rows, l1, dtype):
+    ref64 = x_rows.double() @ l1.double()
+    got = t.cpu().double()
+    err = (got - ref64).abs() / ref64.abs().clamp_min(1e-3 * ref64.abs().max())
+    assert float(err.max()) <= 1.5e-2, float(err.max())
+    ref_bits = oracle.lowrank_down(bits(x_rows.contiguous()), dcode(dtype), bits(l1))
+    mx, mean = rel_errors(oracle.to_f32(bits(t), dcode(dtype)), oracle.to_f32(ref_bits, dcode(dtype)))
+    assert mx <= MAX_REL * 2 and mean <= MEAN_REL, (mx, mean)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K", [(1, 3072), (16, 3072), (17, 3072), (1000, 1280), (4099, 3072), (300, 2048),
+                                 (65, 2560), (33, 1024), (20000, 3072)])
+def test_quant_rows_lowrank_fused(oracle, cuda, dtype, M, K):
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    x = make_x(M, K, dtype, seed=M + K).to(cuda)
+    l1 = _l1(K, 32, dtype, K)
+    qp, s, t = E.quant_rows_lowrank(x, l1.t().contiguous().to(cuda))
+    qr, sr = E.quant_rows_packed(x)
+    assert torch.equal(qp, qr)                                   # padding rows to 16 included
+    assert torch.equal(s.view(torch.int32), sr.view(torch.int32))
+    if M <= 4099:
+        _check_t(oracle, t, x.cpu(), l1, dtype)
+    else:   # large M: t against the separate low-rank kernel (same fp32 accumulation up to order)
+        t2 = E.lowrank_down(x, l1.t().contiguous().to(cuda))
+        mx, mean = rel_errors(t.float().cpu().numpy(), t2.float().cpu().numpy())
+        assert mx <= 1e-2 and mean <= 1e-3, (mx, mean)
+
+
+def test_quant_rows_lowrank_gather_view(oracle, cuda):
+    """Routed gather (duplicates, first and last row) through a row-slice view of a wider activation."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    rows, K, M = 3000, 3072, 1234
+    base = make_x(rows, K + 128, seed=7).to(cuda)
+    x = base[:, 128:]                                            # ldx = K + 128
+    g = torch.Generator().manual_seed(3)
+    idx = torch.randint(0, rows, (M,), generator=g, dtype=torch.int32)
+    idx[:4] = torch.tensor([rows - 1, 0, 0, 5], dtype=torch.int32)
+    l1 = _l1(K, 32, torch.bfloat16, 11)
+    qp, s, t = E.quant_rows_lowrank(x, l1.t().contiguous().to(cuda), idx.to(cuda))
+    qr, sr = E.quant_rows_packed(x, idx.to(cuda))
+    assert torch.equal(qp, qr)
+    assert torch.equal(s, sr)
+    _check_t(oracle, t, x.cpu()[idx.long()], l1, torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,K,R", [(100, 12288, 32), (70, 640, 32), (300, 3072, 64)])
+def test_quant_rows_lowrank_fallback(cuda, M, K, R):
+    """Shapes outside the fused kernel's set run the two kernels: identical to calling them one after the other."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    x = make_x(M, K, seed=K).to(cuda)
+    l1t = _l1(K, R, torch.bfloat16, R).t().contiguous().to(cuda)
+    qp, s, t = E.quant_rows_lowrank(x, l1t)
+    qr, sr = E.quant_rows_packed(x)
+    assert torch.equal(qp, qr) and torch.equal(s, sr)
+    assert torch.equal(t, E.lowrank_down(x, l1t))
+
+
+def test_int8linear_uses_fused_pass(oracle, cuda):
+    """Int8Linear.forward at the c1 shape (reduced M) takes the fused pass: output within the tolerance of the
+    oracle from the same codes, and equal to the GEMM fed with the fused t."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import CONFIGS, make_linear, make_x
+
+    c = CONFIGS["c1"]
+    q = E.Int8Linear(make_linear(c.K, c.N, c.lowrank, c.bias), device=cuda)
+    x = make_x(2000, c.K).to(cuda)
+    y = q(x)
+    qp, sx, t = E.quant_rows_lowrank(x, q.lr_At)
+    ref = E.int8_gemm_packed(qp, sx, q.weight_packed, q.w_scale, q.bias, 2000, c.N, c.K, torch.bfloat16, t=t,
+                             l2t=q.lr_Bt)
+    assert torch.equal(y, ref)
+    o = oracle.linear(bits(x), 0, q.weight_int8.cpu().numpy(), q.w_scale.cpu().numpy(), q.bias.cpu().numpy(), 0,
+                      bits(q.lr_A), bits(q.lr_B))
+    mx, mean = rel_errors(oracle.to_f32(bits(y), 0), o["y"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
