@@ -363,6 +363,18 @@ __device__ __forceinline__ int swz(int r) { return k64_swz(r); }
 template <int N>
 __device__ __forceinline__ void wait_dma() { wait_vmcnt<N>(); }
 
+// The ring's workgroup barrier. A fenced barrier (__syncthreads(), or a fence limited to LDS) makes the compiler
+// wait for every LDS-DMA this wave has in flight (vmcnt(0)), which would drain the ring each stage. Here the
+// ordering is explicit: the caller's vmcnt wait covers the DMA the next stage needs, lgkmcnt(0) completes this
+// wave's LDS reads of the buffer that is about to be refilled, and sched_barrier keeps the scheduler from moving
+// LDS accesses or DMA across the s_barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt and expcnt unconstrained
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // WMW waves along m (2 or 4) times 2 along n; OCC workgroups per CU.
 template <int TI, int TJ, int WMW, int NS, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
 __global__ __attribute__((amdgpu_flat_work_group_size(128 * WMW, 128 * WMW),
@@ -476,9 +488,11 @@ void gemm_dma_kernel(const GemmArgs p) {
   };
 
   // DMA of a stage s >= KT (no operand data left). With ELDS, stage KT brings the row operands of the epilogue and
-  // stage KT + 1 the column operands (slot q: the WG's 16-byte DMA instruction wave * (DW + DA) + i; slots past
-  // the last one repeat it, which rewrites the same bytes); later stages load nothing. Every stage issues DPW
-  // instructions per wave either way, which keeps the vmcnt arithmetic of the ring valid.
+  // stage KT + 1 the column operands: slot q (1 KB at q * 1024 of the stage buffer) is the WG's 16-byte DMA
+  // instruction wave * (DW + DA) + i. Slots past the operands copy the last operand chunk again into their own
+  // (unused) 1 KB, so no instruction repeats another's destination: identical copies into one slot are dead stores
+  // the compiler removes, and a stage issuing fewer than DPW instructions would break the ring's vmcnt arithmetic.
+  // Later stages load nothing (out of range).
   auto dma_tail = [&](int buf, int st) {
     if constexpr (ELDS) {
       if (st == KT || st == KT + 1) {
@@ -502,7 +516,8 @@ void gemm_dma_kernel(const GemmArgs p) {
             LRS ? (void*)lp : (void*)p.s_w, (short)0, lrec, kBufferWord3);
 #pragma unroll
         for (int i = 0; i < DW + DA; ++i) {
-          const int q = min(wave * (DW + DA) + i, nsl - 1);
+          const int qd = wave * (DW + DA) + i;   // destination slot (distinct for every instruction of the WG)
+          const int q = min(qd, nsl - 1);        // source chunk
           int vo = lane * 16;
           __amdgpu_buffer_rsrc_t rs = q == 0 ? rs_v : rs_i;
           if (q >= 2) {
@@ -513,7 +528,7 @@ void gemm_dma_kernel(const GemmArgs p) {
             vo = (int)(row * lrs * 2) + cb;
             rs = rs_l;
           }
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(sb + q * 1024), 16, vo, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(sb + qd * 1024), 16, vo, 0, 0, 0);
         }
         if constexpr (G32) {
 #pragma unroll
@@ -608,20 +623,24 @@ void gemm_dma_kernel(const GemmArgs p) {
   // Ring: stage s lives in buffer s % NS. The DMA of stage s is issued after the barrier of iteration s - NS and
   // must have landed at the barrier that ends iteration s - 1, NS - 1 iterations later; in between, the DMAs of
   // NS - 2 younger stages may still be in flight, hence vmcnt((NS - 2) * DPW).
+  // Prologue: stage 0 alone before the first barrier (the barrier's release fence waits for every LDS-DMA this
+  // wave has in flight), stages 1 .. NS - 1 right after the first fragment reads.
+  if (KT > 0) dma(0, 0);
+  else dma_tail(0, 0);
+  wait_dma<0>();
+  __syncthreads();
+  rd(f0, 0, 0);
 #pragma unroll
-  for (int st = 0; st < NS; ++st) {
+  for (int st = 1; st < NS; ++st) {
     if (st < KT) dma(st, st);
     else dma_tail(st, st);
   }
-  wait_dma<(NS - 1) * DPW>();
-  __syncthreads();
-  rd(f0, 0, 0);
   auto iter = [&](int kt, int b, int bn, auto tail) {
     rd(f1, b, 1);
     mm(f0, kt, 0);
     interleave(no_dma{});
     wait_dma<(NS - 2) * DPW>();   // this wave's DMA of stage kt + 1 has landed
-    __syncthreads();              // every wave's has, and every wave is done reading buffer b
+    lds_barrier();                // every wave's has, and every wave is done reading buffer b
     __builtin_amdgcn_sched_barrier(0);
     rd(f0, bn, 0);
     if constexpr (decltype(tail)::value) dma_tail(b, kt + NS);

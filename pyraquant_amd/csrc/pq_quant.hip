@@ -455,16 +455,15 @@ __global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
   int b = blockIdx.x;
   dma(b);
   for (; b < nbatch; b += G) {
-    // The DMA of batch b was followed only by the NC unconditional code stores of the previous batch (and maybe
-    // the scale and t stores): vmcnt <= NC leaves nothing older than those in flight.
-    wait_vmcnt<NC>();
+    // The DMA of batch b is followed by the previous batch's stores; loads and stores are not guaranteed to
+    // retire in issue order relative to each other, so wait for everything.
+    wait_vmcnt<0>();
     __syncthreads();   // every wave's DMA of batch b has landed
 #pragma unroll
     for (int i = 0; i < NS; ++i) xv[i] = *reinterpret_cast<const v4u*>(xrow + 128 * (i >> 1) + 16 * (i & 1));
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS reads are done
     __syncthreads();                      // every wave's are: the buffer takes the next batch
     dma(b + G < nbatch ? b + G : nbatch);
-    __builtin_amdgcn_sched_barrier(0);   // the stores below stay behind the DMA in the vmcnt queue
 
     const int64_t m = (int64_t)b * 16 + r;
     // absmax: magnitude bits, packed u16 max, then the 4 lanes of the row, then the 4 quarters
@@ -497,7 +496,9 @@ __global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
                                                          __builtin_bit_cast(v8h, xv[i]), acc[h], 0, 0, 0);
       }
     __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();   // amax_l complete (LDS only: the DMA of the next batch stays in flight)
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t am = amax_l[0][r];
 #pragma unroll
     for (int w = 1; w < 4; ++w) am = am > amax_l[w][r] ? am : amax_l[w][r];
@@ -516,7 +517,9 @@ __global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
 #pragma unroll
     for (int h = 0; h < 2; ++h) *reinterpret_cast<v4f*>(&red[wave][r][16 * h + 4 * g]) = acc[h];
     __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();   // red complete
+    __builtin_amdgcn_sched_barrier(0);
     {
       const int mr = tid >> 4, rr = (tid & 15) * 2;
       const int64_t mo = (int64_t)b * 16 + mr;

@@ -234,3 +234,25 @@ def test_gemm_packed_group32_lowrank_scatter(oracle, cuda, lr):
     yo = oracle.epilogue_f32(part, s_row.numpy(), s_w.numpy(), None, bits(t), bits(l2t.t().contiguous()), 1)
     mx, mean = rel_errors(oracle.to_f32(got[r], 1), yo)
     assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
+@pytest.mark.parametrize("M,N,K,lr", [(4352, 12288, 3072, 0), (4352, 12288, 3072, 32), (2100, 9216, 1280, 0)])
+def test_gemm_big_tile_rowmajor_equals_packed_repeated(cuda, M, N, K, lr):
+    """256 x 128 tiles on row-major operands (the reference self-test's int8_gemm_fused shape) give the packed path's
+    bits on every call. The last ring stages carry the epilogue operands; each stage must issue its full DMA count
+    for the ring's vmcnt waits, so a stage that issues fewer leaves the previous stage's last tiles racing."""
+    from pyraquant_amd import int8_exec as E
+
+    a, w = _codes(M, N, K, M + lr, cuda)
+    g = torch.Generator().manual_seed(lr + 3)
+    s_row = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(cuda)
+    s_w = (torch.rand(N, generator=g) * 2e-4 + 1e-5).to(cuda)
+    bias = (torch.randn(N, generator=g) * 0.01).to(cuda)
+    t = l2t = None
+    if lr:
+        t = (torch.randn(M, lr, generator=g) * 0.5).to(torch.bfloat16).to(cuda)
+        l2t = (torch.randn(N, lr, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    ref = E.int8_gemm_packed(E.pack_k64(a), s_row, E.pack_k64(w), s_w, bias, M, N, K, torch.bfloat16, t=t, l2t=l2t)
+    for _ in range(4):
+        y = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, torch.bfloat16)
+        assert torch.equal(y, ref)
