@@ -256,3 +256,33 @@ def test_gemm_big_tile_rowmajor_equals_packed_repeated(cuda, M, N, K, lr):
     for _ in range(4):
         y = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, torch.bfloat16)
         assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_gemm_deep_k_tiles(oracle, cuda, packed):
+    """Long K (>= 8192) on >= 1024 tiles runs 256 x 256 blocks of 8 waves: exact int32 accumulator (int64 row and
+    column checksums, sampled rows against the oracle) and a fused rank-32 output equal to the other layout's."""
+    from pyraquant_amd import int8_exec as E
+
+    M, N, K = 16384, 3072, 12288
+    a, w = _codes(M, N, K, 77, cuda)
+    if packed:
+        c = E.int8_gemm_packed(E.pack_k64(a), None, E.pack_k64(w), None, None, M, N, K, torch.int32)
+    else:
+        c = E.int8_gemm_i32(a, w)
+    rowsum = c.to(torch.int64).sum(dim=1)
+    assert torch.equal(rowsum, (a.to(torch.int64) * w.to(torch.int64).sum(dim=0)[None, :]).sum(dim=1))
+    colsum = c.to(torch.int64).sum(dim=0)
+    assert torch.equal(colsum, (w.to(torch.int64) * a.to(torch.int64).sum(dim=0)[None, :]).sum(dim=1))
+    g = torch.Generator().manual_seed(2)
+    sample = torch.cat([torch.arange(M - 16, M), torch.randperm(M - 16, generator=g)[:16]]).sort().values.to(cuda)
+    assert np.array_equal(c[sample].cpu().numpy(), oracle.gemm_i32(a[sample].cpu().numpy(), w.cpu().numpy()))
+    del c
+    s_row = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(cuda)
+    s_w = (torch.rand(N, generator=g) * 2e-4 + 1e-5).to(cuda)
+    bias = (torch.randn(N, generator=g) * 0.01).to(cuda)
+    t = (torch.randn(M, 32, generator=g) * 0.5).to(torch.bfloat16).to(cuda)
+    l2t = (torch.randn(N, 32, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    yp = E.int8_gemm_packed(E.pack_k64(a), s_row, E.pack_k64(w), s_w, bias, M, N, K, torch.bfloat16, t=t, l2t=l2t)
+    yr = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, torch.bfloat16)
+    assert torch.equal(yp, yr)
