@@ -161,6 +161,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, lin, args.cpu_rows, args.cpu_iters)
+    routing = route_bench(dev, not args.no_cpu) if cfg.routed else None
 
     res = {
         "metric": METRIC,
@@ -192,7 +193,7 @@ def main() -> int:
             "quantizer_alone": {"kernel": "quant_rows_packed", "us": round(qa_ms * 1e3, 1),
                                 "GBps": round(qa_gbs, 1), "frac_hbm": round(qa_gbs / HBM_PEAK_GBS, 4),
                                 "bytes": f"3 M K + 4 M{' + 4 M (gather list)' if rows is not None else ''}"},
-        },
+        } | ({"routing": routing} if routing is not None else {}),
         "roofline": {
             "bound": "mfma",
             "achieved": round(gemm_tops, 2),
@@ -208,6 +209,72 @@ def main() -> int:
     }
     print(json.dumps(res), flush=True)
     return 0
+
+
+def route_bench(dev, with_cpu: bool):
+    """The routed executor's geometry and fusion kernels on config 4's mask (16 x 16-token leaves, 2-token halo,
+    256 x 256 tokens; patches of 32-latent leaves) with FLUX's 64 packed latent channels, bf16: each kernel's
+    average time over 20 calls after 3, HBM bytes per launch and the fraction of 8 TB/s. With with_cpu, the
+    fusion of the oracle's torch CPU restatement (the reference's op sequence, flux/routing.py:328-379) is timed
+    beside it."""
+    import torch
+
+    from pyraquant_amd import routing as RT
+
+    H = W = 256
+    C = 64
+    sel = RT.leaf_mask().to(dev).to(torch.uint8)
+    g = torch.Generator().manual_seed(5)
+    hs = torch.randn(1, H * W, C, generator=g).to(torch.bfloat16).to(dev)
+    bg = torch.randn(H * W, C, generator=g).to(torch.bfloat16).to(dev)
+
+    def timed(fn, n=20):
+        # The calls are queued behind a GPU sleep long enough to cover their host-side launch cost, so the event
+        # pair brackets GPU execution only (these kernels run for microseconds, less than a Python call).
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(20_000_000)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    us_union = timed(lambda: RT.union_rows(sel, 16, 2, (H, W), dev))
+    rt = RT.route_patches(sel, leaf_latent=32, halo_tokens=2, token_hw=(H, W))
+    us_patch = timed(lambda: RT.route_patches(sel, leaf_latent=32, halo_tokens=2, token_hw=(H, W)))
+    info = rt.host()
+    n = info["rows"]
+    dst = torch.empty(n, C, dtype=torch.bfloat16, device=dev)
+    us_gather = timed(lambda: RT.gather_rows(hs[0], rt.rows, rt.counts[1:2], n, out=dst))
+    po = (torch.randn(n, C, generator=g) * 2).to(torch.bfloat16).to(dev)
+    out = torch.empty_like(bg)
+    us_fuse = timed(lambda: RT.fuse_patches(bg, po, rt, fusion_beta=1.0, out=out))
+    gather_bytes = n * (2 * C * 2 + 4)
+    fuse_bytes = 2 * H * W * C * 2 + n * C * 2
+    res = {
+        "mask": "config 4: 103 of 256 leaves, 16 x 16 tokens, halo 2, 256 x 256 tokens, 64 channels bf16",
+        "patches": info["patches"], "patch_rows": n, "buckets": info["buckets"],
+        "union_rows_us": round(us_union, 1), "route_patches_us": round(us_patch, 1),
+        "gather_us": round(us_gather, 1), "gather_GBps": round(gather_bytes / us_gather / 1e3, 1),
+        "fuse_us": round(us_fuse, 1), "fuse_GBps": round(fuse_bytes / us_fuse / 1e3, 1),
+        "fuse_frac_hbm": round(fuse_bytes / us_fuse / 1e3 / HBM_PEAK_GBS, 4),
+        "fuse_bytes": "2 H W C (background) + 2 H W C (out) + 2 rows C (patch predictions), x 2 bytes",
+    }
+    if with_cpu:
+        from oracle import routing_ref as RR
+
+        patches, _ = RR.patch_geometry(RR.route_boxes(sel.cpu(), 32), 2, (H, W))
+        bgc, poc = bg.cpu().view(H, W, C), po.cpu()
+        RR.fuse_patch_predictions(bgc, patches, poc)
+        t0 = time.perf_counter()
+        RR.fuse_patch_predictions(bgc, patches, poc)
+        res["cpu_fuse_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+        res["cpu_fuse_threads"] = torch.get_num_threads()
+    return res
 
 
 def cpu_baseline(cfg, lin, rows: int, iters: int):

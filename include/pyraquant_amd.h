@@ -187,6 +187,67 @@ int pq_dequant_epilogue(const int32_t* acc, const float* s_row, const float* s_c
                         void* c, int64_t ldc, int32_t out_dtype, int64_t M, int64_t N,
                         hipStream_t stream);
 
+/* ---- routed executor: geometry and fusion on the device ------------------------------------------------------
+ * The leaf mask `sel` is uint8 [Lh, Lw] on the device (nonzero = selected; the reference thresholds its mask at
+ * 0.5, flux/run_flux.py:343). Token (y, x) of the H x W packed-token grid is row y * W + x
+ * (flux/routing.py:105-115). Counts are written to device memory, so no call waits for the host.
+ */
+
+/*
+ * Linear-level gather list: the sorted, unique token rows covered by the union of the selected leaves
+ * (leaf_tokens x leaf_tokens tokens each), each dilated by `halo` tokens and clamped to the grid
+ * (flux/routing.py:235-244). rows holds up to H * W entries; *count receives their number. Requires
+ * Lh * leaf_tokens <= H, Lw * leaf_tokens <= W, Lw <= 64, Lh <= 1024 and Lh * Lw <= 32768. The reference builds its row sets on the host
+ * from sel.cpu() (flux/run_flux.py:343-355, flux/routing.py:253-315); this list is the union of those patches.
+ */
+int pq_route_union_rows(const uint8_t* sel, int64_t Lh, int64_t Lw, int64_t leaf_tokens, int64_t halo, int64_t H,
+                        int64_t W, int32_t* rows, int32_t* count, hipStream_t stream);
+
+/*
+ * Patch extraction geometry of the routed executor:
+ *   boxes  : row-wise runs of selected leaves, leaf_latent latent cells each (flux/run_flux.py:340-355);
+ *   cores  : latent box -> packed-token box with the 2x2 packing phase packing_offset (flux/routing.py:202-232);
+ *            repeated cores are dropped (:276-278);
+ *   patches: core dilated by `halo` tokens, clamped (:235-244), grouped by shape in ascending (h, w) order, box
+ *            order inside a shape (:298-315).
+ * table [patches, 12] int32, per patch in extraction order: halo box oy0, oy1, ox0, ox1; core box cy0, cy1, cx0,
+ * cx1; first row of the patch in `rows`; source box index; bucket (shape rank); 0. Room for Lh * ceil(Lw / 2)
+ * patches. counts[4] int32: patches, rows, buckets, error bits (1 = more than max_rows rows; those patches' rows
+ * are not written). rows [max_rows] int32: every patch's token rows, row-major inside the patch, patches in
+ * order -- the order in which build_patch_buckets stacks hidden_states (:286-296). max_rows = 0 computes the
+ * table only. Requires leaf_latent even, Lh <= 1024, Lh * Lw <= 32768, Lh * ceil(Lw / 2) <= 2048, H, W <= 32767
+ * and the leaf grid inside the token grid.
+ */
+int pq_route_patches(const uint8_t* sel, int64_t Lh, int64_t Lw, int64_t leaf_latent, int64_t halo, int64_t H,
+                     int64_t W, int64_t packing_offset, int32_t* table, int32_t* counts, int32_t* rows,
+                     int64_t max_rows, hipStream_t stream);
+
+/*
+ * Row gather with a device-side count: dst row r = src row rows[r] for r < min(*count, n_max), row_bytes bytes per
+ * row (multiple of 4), strides in bytes. The patch extraction of hidden_states / img_ids in build_patch_buckets
+ * (flux/routing.py:286-296), without the host learning the row count.
+ */
+int pq_gather_rows(const void* src, int64_t ld_src_bytes, const int32_t* rows, const int32_t* count, int64_t n_max,
+                   int64_t row_bytes, void* dst, int64_t ld_dst_bytes, hipStream_t stream);
+
+/*
+ * Feathered fusion of the patch predictions into the background (fuse_patch_predictions, flux/routing.py:328-379,
+ * with halo_feather_mask :34-75, min_alpha 0):
+ *   per patch covering a token, in table order: beta = (fusion_beta * mask).clamp(0, 1);
+ *   local += beta * out; beta_acc += beta  (every product and sum rounded to the 16-bit type, as torch does);
+ *   result = (1 - clamp(beta_acc, 0, 1)) * bg + clamp(beta_acc, 0, 1) * where(beta_acc > 0, local / beta_acc, 0).
+ * mask = min(y ramp, x ramp) over the halo, 1 over the core. ramp holds, for every ramp length m = 1 .. halo
+ * (the halo of the route table, at most 64), the
+ * rising ramp r(linspace(0, 1, m)) and the falling ramp r(linspace(1, 0, m)) interleaved:
+ * ramp[2 (m (m - 1) / 2 + u)] and ramp[2 (m (m - 1) / 2 + u) + 1] (fp32; the caller evaluates the reference's
+ * _smooth_ramp, flux/routing.py:21-31, once per halo and mode). background / out [H * W, C] (row strides ldb /
+ * ldo), patch_out [rows, C] (row stride ldp) holds the patch predictions in the order of `rows` from
+ * pq_route_patches; table / counts from pq_route_patches. C % 8 == 0, 16-byte aligned rows, dtype bf16 or fp16.
+ */
+int pq_fuse_patches(const void* background, int64_t ldb, const void* patch_out, int64_t ldp, const int32_t* table,
+                    const int32_t* counts, const float* ramp, int64_t halo, float fusion_beta, int64_t H, int64_t W,
+                    int64_t C, int32_t dtype, void* out, int64_t ldo, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

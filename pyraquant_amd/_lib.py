@@ -32,6 +32,10 @@ EXPORTS = (
     "pq_quant_rows_packed",
     "pq_quant_rows_lowrank",
     "pq_dequant_epilogue",
+    "pq_route_union_rows",
+    "pq_route_patches",
+    "pq_gather_rows",
+    "pq_fuse_patches",
 )
 
 _p = ctypes.c_void_p
@@ -54,6 +58,11 @@ _SIGNATURES = {
     "pq_quant_rows_packed": ([_p, _i32, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
     "pq_quant_rows_lowrank": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p], ctypes.c_int),
     "pq_dequant_epilogue": ([_p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p], ctypes.c_int),
+    "pq_route_union_rows": ([_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "pq_route_patches": ([_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p], ctypes.c_int),
+    "pq_gather_rows": ([_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p], ctypes.c_int),
+    "pq_fuse_patches": ([_p, _i64, _p, _i64, _p, _p, _p, _i64, ctypes.c_float, _i64, _i64, _i64, _i32, _p, _i64, _p],
+                        ctypes.c_int),
 }
 
 _lib = None

@@ -82,6 +82,24 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, 8, nul, p16, 24, p16, 32, nul) == L.PQ_ESHAPE
     assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, 4, nul, p16, 32, p16, 32, nul) == L.PQ_ESHAPE   # x_rows < M
     assert lib.pq_dequant_epilogue(nul, nul, nul, nul, nul, 128, 0, 8, 128, nul) == L.PQ_EINVAL
+    # routing geometry and fusion
+    assert lib.pq_route_union_rows(nul, 16, 16, 16, 2, 256, 256, p16, p16, nul) == L.PQ_EINVAL
+    assert lib.pq_route_union_rows(p16, 16, 16, 16, 2, 200, 256, p16, p16, nul) == L.PQ_ESHAPE   # leaves past H
+    assert lib.pq_route_union_rows(p16, 16, 16, 16, -1, 256, 256, p16, p16, nul) == L.PQ_ESHAPE
+    assert lib.pq_route_patches(p16, 8, 8, 63, 8, 256, 256, 0, p16, p16, p16, 100, nul) == L.PQ_EINVAL  # odd leaf
+    assert lib.pq_route_patches(p16, 8, 8, 64, 8, 256, 256, 2, p16, p16, p16, 100, nul) == L.PQ_EINVAL  # offset
+    assert lib.pq_route_patches(p16, 8, 8, 64, 8, 255, 256, 0, p16, p16, p16, 100, nul) == L.PQ_ESHAPE
+    assert lib.pq_route_patches(p16, 64, 128, 4, 1, 256, 256, 0, p16, p16, p16, 100, nul) == L.PQ_ESHAPE  # boxes
+    assert lib.pq_gather_rows(p16, 12, p16, p16, 10, 6, p16, 12, nul) == L.PQ_EALIGN
+    assert lib.pq_gather_rows(p16, 12, p16, p16, 0, 12, p16, 12, nul) == L.PQ_OK
+    fuse = lambda C, beta, dt, ldb, halo=2: lib.pq_fuse_patches(p16, ldb, p16, C, p16, p16, p16, halo, beta, 16, 16,
+                                                                C, dt, p16, C, nul)
+    assert fuse(12, 1.0, 0, 12) == L.PQ_ESHAPE           # C % 8
+    assert fuse(16, 1.5, 0, 16) == L.PQ_EINVAL           # fusion_beta outside [0, 1]
+    assert fuse(16, 1.0, 0, 20) == L.PQ_EALIGN
+    assert fuse(16, 1.0, 2, 16) == L.PQ_EDTYPE
+    assert fuse(16, 1.0, 0, 16, halo=65) == L.PQ_EINVAL
+    assert lib.pq_route_union_rows(p16, 4, 65, 4, 1, 256, 260, p16, p16, nul) == L.PQ_ESHAPE   # > 64 leaf columns
 
 
 def test_status_codes_map_to_reference_exceptions(lib):

@@ -285,18 +285,24 @@ def test_linear_golden_codes_and_output(oracle):
 
 
 # ------------------------------------------------------------------------------------------- I. routing
+def _c4_mask():
+    rec = json.load(open(os.path.join(GOLD, "route_c4.json")))
+    return rec, np.array([[c == "1" for c in r] for r in rec["mask_rows"]])
+
+
 def test_route_rows_c4_golden(oracle):
-    """Config-4 row set: C brute force, numpy box arithmetic and the golden record agree (count, hash)."""
+    """Config-4 row set: the C brute force, the union of the restated patch geometry (flux/routing.py:253-315) and
+    the golden record agree (count, hash); the leaf map is the seeded Bernoulli(0.35) of the record."""
+    from oracle import routing_ref as RR
     from pyraquant_amd import routing
 
-    rec = json.load(open(os.path.join(GOLD, "route_c4.json")))
+    rec, mask = _c4_mask()
     sel = routing.leaf_mask()
     assert int(sel.sum()) == rec["active_leaves"] == 103
-    mask = np.array([[c == "1" for c in r] for r in rec["mask_rows"]])
     assert np.array_equal(sel.numpy(), mask)
     rows_c = oracle.route_rows_union(mask.astype(np.uint8), 16, 2)
-    rows_py = routing.routed_row_index(sel).numpy()
-    assert np.array_equal(rows_c, rows_py)
+    _, prow = RR.patch_geometry(RR.route_boxes(mask, 32), 2, (256, 256))
+    assert np.array_equal(rows_c, np.unique(prow))
     assert rows_c.size == rec["union_rows"] == 33316
     assert hashlib.sha256(rows_c.astype("<i4").tobytes()).hexdigest() == rec["sha256_int32_le"]
     assert np.all(np.diff(rows_c) > 0)
@@ -318,26 +324,142 @@ def test_route_rows_small_cases(oracle):
     assert oracle.route_rows_union(m, 16, 2).size == 20 * 36
 
 
-def test_route_patch_order(oracle):
-    """patches mode (flux/routing.py:253-315 order) covers exactly the union's rows, with halo overlaps
-    duplicated across patches, and every patch row-major."""
-    from pyraquant_amd import routing
+def test_route_boxes_and_patch_order():
+    """Row-run boxes (flux/run_flux.py:340-355) of a hand mask, and the extraction order of flux/routing.py:253-315:
+    shapes ascending, box order inside a shape, rows row-major, halo overlaps repeated."""
+    from oracle import routing_ref as RR
 
-    sel = routing.leaf_mask()
-    union = routing.routed_row_index(sel, mode="union").numpy()
-    patches = routing.routed_row_index(sel, mode="patches").numpy()
-    assert np.array_equal(np.unique(patches), union)
-    assert patches.size >= union.size
+    m = np.array([[0, 1, 1, 0, 1],
+                  [1, 1, 1, 1, 1],
+                  [0, 0, 0, 0, 1]], bool)
+    boxes = RR.route_boxes(m, 8)
+    assert boxes == [(0, 8, 8, 24), (0, 8, 32, 40), (8, 16, 0, 40), (16, 24, 32, 40)]
+    patches, rows = RR.patch_geometry(boxes, 1, (12, 20))
+    # token cores (latent / 2): (0,4,4,12) (0,4,16,20) (4,8,0,20) (8,12,16,20); halo 1 clamped to the 12 x 20
+    # grid gives shapes 5x10, 5x5, 6x20, 5x5: buckets (5,5) (5,5) (5,10) (6,20)
+    shapes = [(p["halo"][1] - p["halo"][0], p["halo"][3] - p["halo"][2]) for p in patches]
+    assert shapes == sorted(shapes)
+    assert [p["box_index"] for p in patches] == [1, 3, 0, 2]
+    assert patches[0]["halo"] == (0, 5, 15, 20) and patches[0]["inner"] == (0, 4, 1, 5)
+    assert [p["bucket"] for p in patches] == [0, 0, 1, 2]
+    assert rows.size == sum(h * w for h, w in shapes)
+    assert list(rows[:5]) == [15, 16, 17, 18, 19]          # first patch, first row, row-major
+    # the c4 mask: the patch rows cover the union exactly, with overlaps repeated
+    _, mask = _c4_mask()
+    _, prow = RR.patch_geometry(RR.route_boxes(mask, 32), 2, (256, 256))
+    assert prow.size > np.unique(prow).size
 
 
 def test_unpacked_box_errors():
-    """Validation of flux/routing.py:202-232: negative, odd and empty boxes raise ValueError."""
-    from pyraquant_amd.routing import unpacked_box_to_token_box
+    """Validation of flux/routing.py:202-232: negative, odd and empty boxes raise ValueError; offset 1 covers both
+    straddling tokens."""
+    from oracle import routing_ref as RR
 
-    assert unpacked_box_to_token_box((0, 4, 2, 8)) == (0, 2, 1, 4)
+    assert RR.token_box((0, 4, 2, 8)) == (0, 2, 1, 4)
+    assert RR.token_box((0, 4, 2, 8), 1) == (0, 3, 1, 5)
     for bad in ((-2, 4, 0, 4), (1, 4, 0, 4), (4, 4, 0, 4)):
         with pytest.raises(ValueError):
-            unpacked_box_to_token_box(bad)
+            RR.token_box(bad)
+
+
+def test_feather_ramp_closed_form():
+    """The cosine ramp is 0.5 - 0.5 cos(pi u) on linspace points (float64 closed form within fp32 rounding), starts
+    at 0, ends at 1, and the falling ramp mirrors the rising one except at length 1; the mask is 1 over the core and min of the two
+    edge ramps in a halo corner."""
+    import torch
+
+    from oracle import routing_ref as RR
+
+    for m in range(1, 9):
+        up = RR.smooth_ramp(torch.linspace(0.0, 1.0, m)).double().numpy()
+        dn = RR.smooth_ramp(torch.linspace(1.0, 0.0, m)).double().numpy()
+        u = np.linspace(0.0, 1.0, m)
+        assert np.allclose(up, 0.5 - 0.5 * np.cos(np.pi * u), atol=3e-7)
+        if m == 1:   # linspace(0, 1, 1) = [0] but linspace(1, 0, 1) = [1]: a 1-token falling halo keeps weight 1
+            assert up[0] == 0.0 and dn[0] == 1.0
+            continue
+        assert np.allclose(dn, up[::-1], atol=3e-7)
+        assert up[0] == 0.0 and up[-1] == 1.0
+    mask = RR.halo_feather_mask((8, 10), (3, 6, 2, 8), torch.float32).numpy()
+    assert np.all(mask[3:6, 2:8] == 1.0)
+    yr = RR.smooth_ramp(torch.linspace(0.0, 1.0, 3)).numpy()
+    xr = RR.smooth_ramp(torch.linspace(0.0, 1.0, 2)).numpy()
+    assert mask[1, 1] == min(yr[1], xr[1]) and mask[0, 5] == 0.0 and mask[4, 0] == 0.0
+
+
+def _fusion_case(seed, H=24, W=28, C=16, dtype=None, halo=3):
+    import torch
+
+    from oracle import routing_ref as RR
+
+    dtype = dtype or torch.bfloat16
+    g = torch.Generator().manual_seed(seed)
+    m = (torch.rand(3, 3, generator=g) < 0.5).numpy()
+    m[1, 1] = True
+    patches, rows = RR.patch_geometry(RR.route_boxes(m, 16), halo, (H, W))
+    bg = torch.randn(H, W, C, generator=g).to(dtype)
+    po = torch.randn(rows.size, C, generator=g).to(dtype)
+    return RR, patches, rows, bg, po
+
+
+def test_fusion_closed_forms():
+    """fuse_patch_predictions: no patch -> background bits; fusion_beta 0 -> background; a token inside exactly one
+    core -> that patch's prediction bits; two equal full weights -> their mean within one rounding."""
+    import torch
+
+    RR, patches, rows, bg, po = _fusion_case(1)
+    H, W, C = bg.shape
+    assert torch.equal(RR.fuse_patch_predictions(bg, [], po[:0]), bg)
+    assert torch.equal(RR.fuse_patch_predictions(bg, patches, po, fusion_beta=0.0), bg)
+    out = RR.fuse_patch_predictions(bg, patches, po)
+    cover = np.zeros((H, W), int)
+    for p in patches:
+        y0, y1, x0, x1 = p["halo"]
+        cover[y0:y1, x0:x1] += 1
+    off = 0
+    for p in patches:
+        y0, y1, x0, x1 = p["halo"]
+        cy0, cy1, cx0, cx1 = p["core"]
+        pw = x1 - x0
+        for y in range(cy0, cy1):
+            for x in range(cx0, cx1):
+                if cover[y, x] == 1:
+                    assert torch.equal(out[y, x], po[off + (y - y0) * pw + (x - x0)])
+        off += (y1 - y0) * pw
+    assert torch.equal(out[cover == 0], bg[torch.from_numpy(cover == 0)])
+    # two identical patches over the same core: the blend of a prediction with itself is that prediction
+    two = [patches[0], patches[0]]
+    n0 = (patches[0]["halo"][1] - patches[0]["halo"][0]) * (patches[0]["halo"][3] - patches[0]["halo"][2])
+    o2 = RR.fuse_patch_predictions(bg, two, torch.cat([po[:n0], po[:n0]]))
+    y0, y1, x0, x1 = patches[0]["core"]
+    ref = out if cover[y0:y1, x0:x1].max() == 1 else None
+    if ref is not None:
+        assert torch.equal(o2[y0:y1, x0:x1], ref[y0:y1, x0:x1])
+
+
+def test_fusion_against_float64_blend():
+    """The op-by-op 16-bit fusion stays within a few 16-bit roundings of the float64 blend
+    (1 - b) bg + b (sum beta_i out_i / sum beta_i), b = min(sum beta_i, 1), for bf16 and fp16."""
+    import torch
+
+    for dt, tol in ((torch.bfloat16, 4 * 2.0 ** -8), (torch.float16, 4 * 2.0 ** -11)):
+        RR, patches, rows, bg, po = _fusion_case(7, dtype=dt)
+        H, W, C = bg.shape
+        out = RR.fuse_patch_predictions(bg, patches, po).double()
+        num = torch.zeros(H, W, C, dtype=torch.float64)
+        den = torch.zeros(H, W, 1, dtype=torch.float64)
+        off = 0
+        for p in patches:
+            y0, y1, x0, x1 = p["halo"]
+            ph, pw = y1 - y0, x1 - x0
+            beta = RR.halo_feather_mask((ph, pw), p["inner"], torch.float64)[:, :, None]
+            num[y0:y1, x0:x1] += beta * po[off:off + ph * pw].double().reshape(ph, pw, C)
+            den[y0:y1, x0:x1] += beta
+            off += ph * pw
+        b = den.clamp(0, 1)
+        ref = (1 - b) * bg.double() + b * torch.where(den > 0, num / den.clamp_min(1e-30), torch.zeros_like(num))
+        scale = ref.abs().clamp_min(1.0)
+        assert float(((out - ref).abs() / scale).max()) <= tol
 
 
 # ------------------------------------------------------------------------------------------- planted mistakes
