@@ -8,11 +8,12 @@
 // of 8 elements per lane), so x is read from HBM exactly once. The absmax is a packed-u16 max over the
 // magnitude bits (monotonic in |x| for finite 16-bit floats) and a wave reduction.
 //
-// Exact codes without one IEEE division per element: with c = fl(1/s) and r = fl(x * c),
-// |r - fl(x / s)| <= 3 * 2^-24 * 127 < 2.3e-5, so whenever r is farther than kTieMargin from every
-// half-integer, rint(r) == rint(fl(x / s)). rint(r) comes from the 1.5 * 2^23 magic add (round to nearest
-// even in the fp32 adder), whose low byte is the int8 code. Lanes that land within the margin (about one
-// element in 10^4) redo that element with the correctly rounded division.
+// Exact codes without one IEEE division per element: with c = fl(1/s) and v = x * c (exact product),
+// |v - x / s| <= |x| |c - 1/s| <= 127 * 2^-24 and |x / s - fl(x / s)| <= 127 * 2^-24, so |v - fl(x / s)| < 1.6e-5:
+// whenever v is farther than kTieMargin from every half-integer, rint(v) == rint(fl(x / s)). One fma gives
+// m = fl(v + 1.5 * 2^23) = 1.5 * 2^23 + rint(v) (round to nearest even; |v| < 2^22), whose low byte is the int8
+// code, and a second gives the residual fl(v - rint(v)), whose largest magnitude over 8 elements is tested once.
+// Chunks with an element within the margin (about one element in 10^4) redo it with the correctly rounded division.
 #include "pq_common.h"
 
 #include <algorithm>
@@ -24,7 +25,7 @@ namespace pq {
 namespace {
 
 constexpr float kMagic = 12582912.0f;        // 1.5 * 2^23: x + kMagic rounds x to an integer (|x| < 2^22)
-constexpr float kTieMargin = 6.0e-5f;        // > 2.3e-5 error bound of r, see the header comment
+constexpr float kTieMargin = 6.0e-5f;        // > 1.6e-5 error bound of v, see the header comment
 constexpr float kNearHalf = 0.5f - kTieMargin;
 
 // Code of one element: returns kMagic + q as fp32 (its low byte is the int8 code q).
@@ -34,10 +35,11 @@ __device__ __forceinline__ float code_exact(float x, float s) {
   return q + kMagic;
 }
 
+// Low bytes of four fp32 bit patterns packed into one dword (three byte permutes).
 __device__ __forceinline__ uint32_t low_bytes4(float m0, float m1, float m2, float m3) {
-  uint32_t b0 = __float_as_uint(m0) & 0xffu, b1 = __float_as_uint(m1) & 0xffu;
-  uint32_t b2 = __float_as_uint(m2) & 0xffu, b3 = __float_as_uint(m3) & 0xffu;
-  return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+  const uint32_t a = __builtin_amdgcn_perm(__float_as_uint(m1), __float_as_uint(m0), 0x0c0c0400u);   // m0.b0 m1.b0
+  const uint32_t b = __builtin_amdgcn_perm(__float_as_uint(m3), __float_as_uint(m2), 0x0c0c0400u);   // m2.b0 m3.b0
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
 }
 
 // Quantize 8 elements held in one 16-byte chunk; returns 8 int8 codes packed in a uint2.
@@ -49,20 +51,16 @@ __device__ __forceinline__ v2u quant_chunk(v4u v, float s, float rc) {
   f[4] = lo16_to_f32<DT>(v.z); f[5] = hi16_to_f32<DT>(v.z);
   f[6] = lo16_to_f32<DT>(v.w); f[7] = hi16_to_f32<DT>(v.w);
   float m[8];
-  bool near_tie = false;
+  float d = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float r = f[i] * rc;
-    m[i] = r + kMagic;
-    const float d = fabsf(r - (m[i] - kMagic));
-    near_tie |= d > kNearHalf;
+    m[i] = __builtin_fmaf(f[i], rc, kMagic);
+    d = fmaxf(d, fabsf(__builtin_fmaf(f[i], rc, -(m[i] - kMagic))));
   }
-  if (__builtin_expect(near_tie, 0)) {
+  if (__builtin_expect(d > kNearHalf, 0)) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float r = f[i] * rc;
-      if (fabsf(r - (m[i] - kMagic)) > kNearHalf) m[i] = code_exact(f[i], s);
-    }
+    for (int i = 0; i < 8; ++i)
+      if (fabsf(__builtin_fmaf(f[i], rc, -(m[i] - kMagic))) > kNearHalf) m[i] = code_exact(f[i], s);
   }
   return v2u{low_bytes4(m[0], m[1], m[2], m[3]), low_bytes4(m[4], m[5], m[6], m[7])};
 }
