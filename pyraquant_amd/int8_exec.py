@@ -193,6 +193,17 @@ def int8_gemm_i32(xq: torch.Tensor, w_int8: torch.Tensor) -> torch.Tensor:
 
 
 # --------------------------------------------------------------------------- packed K64 layer path
+# Int8Linear.forward's direct path (one workspace allocation, raw pointers); False routes every call through the
+# general wrappers (same kernels, same bits).
+DIRECT_CALLS = True
+_DIRECT_DTYPES = {torch.bfloat16: _lib.PQ_BF16, torch.float16: _lib.PQ_F16}
+
+
+def _raw_stream(dev: torch.device) -> int:
+    """The current HIP stream of `dev` as an integer handle."""
+    return torch._C._cuda_getCurrentRawStream(dev.index if dev.index is not None else torch.cuda.current_device())
+
+
 def packed_rows(rows: int) -> int:
     """Rows of a packed K64 buffer holding `rows` rows (a multiple of 16)."""
     return (rows + 15) // 16 * 16
@@ -398,10 +409,57 @@ class Int8Linear(nn.Module):
             return self.lr_Bt.to(dtype)
         return self.lr_Bt
 
+    def _forward_direct(self, x: torch.Tensor) -> Optional[torch.Tensor]:
+        """The common layer call (no routing arguments, packed weights) with the host work cut to the two C calls:
+        codes, scales and t share one workspace allocation, operands go as raw pointers, the stream is the raw
+        current stream. Same kernels and arguments as the general path, so the same bits; returns None when a
+        precondition of this path does not hold."""
+        dt = x.dtype
+        code = _DIRECT_DTYPES.get(dt)
+        K, N = self.in_features, self.out_features
+        if code is None or x.device != self.weight_packed.device or x.shape[-1] != K:
+            return None
+        x2 = x.reshape(-1, K)
+        if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            return None
+        R = 0 if self.lr_At is None else self.lr_At.shape[0]
+        if R and (self.lr_At.dtype != dt or self.lr_Bt.dtype != dt):
+            return None
+        M = x2.shape[0]
+        dev = x2.device
+        q_bytes = packed_rows(M) * K
+        s_off = (q_bytes + 255) & ~255
+        t_off = s_off + ((4 * M + 255) & ~255)
+        ws = torch.empty(t_off + 2 * M * R, dtype=torch.uint8, device=dev)
+        out = torch.empty((M, N), dtype=dt, device=dev)
+        base = ws.data_ptr()
+        stream = _raw_stream(dev)
+        L = _lib.load()
+        if R:
+            st = L.pq_quant_rows_lowrank(x2.data_ptr(), code, M, K, x2.stride(0), M, None, self.lr_At.data_ptr(), R,
+                                         base, base + s_off, base + t_off, R, stream)
+            what = "quant_rows_lowrank"
+        else:
+            st = L.pq_quant_rows_packed(x2.data_ptr(), code, M, K, x2.stride(0), None, base, base + s_off, stream)
+            what = "quant_rows_packed"
+        if st:
+            _lib.check(st, what)
+        st = L.pq_int8_gemm_packed(base, self.weight_packed.data_ptr(), base + s_off, self._scale_k().data_ptr(),
+                                   self.group_size, None if self.bias is None else self.bias.data_ptr(),
+                                   base + t_off if R else None, R, self.lr_Bt.data_ptr() if R else None, R,
+                                   code, out.data_ptr(), N, code, None, M, N, K, stream)
+        if st:
+            _lib.check(st, "int8_gemm_packed")
+        return out.reshape(*x.shape[:-1], N)
+
     def forward(self, x: torch.Tensor, row_idx: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
         """y = Linear(x) through quantizer (+ low-rank down) + fused GEMM (deploy/int8_exec.py:382-408).
         Routed use: ``row_idx`` gathers rows of x (2-D x only), ``out``/``out_row_idx`` scatter into a canvas."""
+        if row_idx is None and out is None and out_row_idx is None and self.weight_packed is not None and DIRECT_CALLS:
+            y = self._forward_direct(x)
+            if y is not None:
+                return y
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
         if x2.stride(1) != 1:

@@ -215,3 +215,63 @@ def test_lowrank_down_dma_and_fallback(oracle, cuda, M, K, R, gather):
     ref_bits = oracle.lowrank_down(bits(x.contiguous()), 0, bits(l1), None if idx is None else idx.numpy())
     mx, mean = rel_errors(oracle.to_f32(bits(t), 0), oracle.to_f32(ref_bits, 0))
     assert mx <= MAX_REL * 2 and mean <= MEAN_REL, (mx, mean)
+
+
+@pytest.mark.parametrize("K,N,R,group,dtype,M", [(3072, 3072, 32, 0, torch.bfloat16, 2048),
+                                                 (640, 640, 0, 0, torch.float16, 2048),
+                                                 (1280, 1280, 0, 32, torch.float16, 154),
+                                                 (3072, 12288, 32, 0, torch.bfloat16, 17),
+                                                 (2560, 640, 32, 0, torch.float16, 1)])
+def test_int8linear_direct_path_matches_general(cuda, K, N, R, group, dtype, M):
+    """Int8Linear.forward's direct path (one workspace, raw pointers) returns the same bits as the general
+    wrappers, for 2-D and 3-D inputs."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    lin = make_linear(K, N, R, True, dtype=dtype)
+    q = E.Int8Linear(lin, device=cuda, group_size=group)
+    x = make_x(M, K, dtype, seed=K + M).to(cuda)
+    y_direct = q(x)
+    y3 = q(x.reshape(1, M, K))
+    E.DIRECT_CALLS = False
+    try:
+        y_general = q(x)
+    finally:
+        E.DIRECT_CALLS = True
+    assert torch.equal(y_direct, y_general)
+    assert torch.equal(y3.reshape(M, N), y_general)
+
+
+def test_int8linear_graph_replay(cuda):
+    """A chain of Int8Linear forwards captured in a HIP graph (torch.cuda.graph) replays to the eager bits, replay
+    after replay, with eager work and synchronisation between replays: the kernels allocate and clear nothing
+    themselves, so a captured layer is launch-overhead free."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    a = E.Int8Linear(make_linear(1280, 5120, 32, True, dtype=torch.float16), device=cuda)
+    b = E.Int8Linear(make_linear(5120, 1280, 0, True, dtype=torch.float16), device=cuda, group_size=32)
+    x = make_x(2048, 1280, torch.float16).to(cuda)
+    static_x = x.clone()
+    ref = b(a(x))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            b(a(static_x))
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_y = b(a(static_x))
+    for i in range(4):
+        noise = make_x(2048, 1280, torch.float16, seed=100 + i).to(cuda)
+        eager_other = b(a(noise))             # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_y, ref), i
+        assert torch.equal(eager_other, b(a(noise))), i
+    static_x.copy_(make_x(2048, 1280, torch.float16, seed=7).to(cuda))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(static_y, b(a(static_x)))
