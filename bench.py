@@ -162,6 +162,7 @@ def main() -> int:
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, lin, args.cpu_rows, args.cpu_iters)
     routing = route_bench(dev, not args.no_cpu) if cfg.routed else None
+    launch = launch_bench(dev) if cfg.group else None
 
     res = {
         "metric": METRIC,
@@ -193,7 +194,7 @@ def main() -> int:
             "quantizer_alone": {"kernel": "quant_rows_packed", "us": round(qa_ms * 1e3, 1),
                                 "GBps": round(qa_gbs, 1), "frac_hbm": round(qa_gbs / HBM_PEAK_GBS, 4),
                                 "bytes": f"3 M K + 4 M{' + 4 M (gather list)' if rows is not None else ''}"},
-        } | ({"routing": routing} if routing is not None else {}),
+        } | ({"routing": routing} if routing is not None else {}) | ({"small_m_launch": launch} if launch else {}),
         "roofline": {
             "bound": "mfma",
             "achieved": round(gemm_tops, 2),
@@ -209,6 +210,57 @@ def main() -> int:
     }
     print(json.dumps(res), flush=True)
     return 0
+
+
+def launch_bench(dev):
+    """SDXL's 1K stage (M = 2048 tokens) over its token-level (K, N) shapes, group-32 fp16 Int8Linear: per-layer GPU
+    time (50 calls queued behind a GPU sleep), host time per eager call (200 calls, no synchronisation inside), and
+    the per-layer time of a HIP graph of 10 captured calls replayed (deploy/run_sdxl_latency.py:144-147 quotes the
+    reference's per-call launch overhead at this M)."""
+    import torch
+
+    from pyraquant_amd import sdxl
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    M = 2048
+    rows = []
+    for K, N in sdxl.SDXL_TOKEN_SHAPES:
+        q = sdxl.SdxlInt8Linear(make_linear(K, N, 0, True, dtype=torch.float16), device=dev, group_size=32)
+        x = make_x(M, K, torch.float16, seed=K + N).to(dev)
+        for _ in range(5):
+            y = q(x)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(50_000_000)
+        e0.record()
+        for _ in range(50):
+            y = q(x)
+        e1.record()
+        torch.cuda.synchronize()
+        gpu = e0.elapsed_time(e1) / 50 * 1e3
+        t0 = time.perf_counter()
+        for _ in range(200):
+            y = q(x)
+        host = (time.perf_counter() - t0) / 200 * 1e6
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            y = q(x)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ys = [q(x) for _ in range(10)]
+        g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(20):
+            g.replay()
+        torch.cuda.synchronize()
+        graph = (time.perf_counter() - t0) / 200 * 1e6
+        rows.append({"K": K, "N": N, "gpu_us": round(gpu, 1), "host_us_per_eager_call": round(host, 1),
+                     "graph_us_per_call": round(graph, 1), "graph_equals_eager": bool(torch.equal(ys[-1], y))})
+    return {"M": M, "dtype": "fp16 in/out, group-32 weights, bias", "layers": rows}
 
 
 def route_bench(dev, with_cpu: bool):
