@@ -11,10 +11,10 @@
 //
 // The kernel (gemm_dma_kernel). 2 x WMW wavefronts (WMW = 2 or 4 along m). A workgroup owns a BN x BM (n x m)
 // block, each wave a (BN/2) x (BM/WMW) part held as TI x TJ v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in
-// AGPRs). Large problems run 256 x 128 blocks of 4 waves at two workgroups per CU (128 accumulators per wave, so two
-// waves share a SIMD and one workgroup's epilogue overlaps the other's MFMAs), or for long K 256 x 256 blocks of 8
-// waves at one per CU; small ones 128 x 128, also two per CU.
-// K advances in stages of 64 bytes through a ring of NS LDS stages (3 x 24 KB per workgroup at two per CU) filled by
+// AGPRs). Large problems run 256 x 256 blocks of 8 waves at one workgroup per CU (128 accumulators per wave, two
+// waves per SIMD); small ones 128 x 128 blocks of 4 waves at two workgroups per CU, or 128 x 64 when the 128 x 128
+// blocks are too few to fill the chip.
+// K advances in stages of 64 bytes through a ring of NS LDS stages (5 x 32 KB for the 256 x 256 block) filled by
 // LDS-DMA buffer loads (buffer_load_dwordx4 ... lds): no VGPR staging, no ds_write, and NS - 1 stages of
 // prefetch in flight to cover L2 / MALL latency. One DMA instruction fills 1 KB = 16 LDS rows of 64 bytes;
 // each lane fetches the 16-byte chunk that the XOR swizzle places at its LDS slot, so the MFMA operand reads
@@ -713,17 +713,15 @@ int launch_dma(GemmArgs& a, hipStream_t stream) {
   return check_launch("int8_gemm");
 }
 
-// Tile choice of the LDS-DMA kernel: 256 x 128 (n x m) blocks at two workgroups per CU when they fill the 512
-// workgroup slots at least twice (one workgroup's epilogue, barriers and first-stage latency then overlap the other's
-// MFMAs), else 128 x 128 blocks, also two per CU (measured 17 % faster than one per CU at M = 4096, K = N = 3072). For long K (deep_k), where the epilogue is a small share of a tile,
-// 256 x 256 blocks of 8 waves at one workgroup per CU: a third less LDS-DMA traffic per MFMA than two 256 x 128
-// workgroups, at the price of an epilogue that no other workgroup overlaps (measured: 6 % faster at K = 12288,
-// about even at K = 3072).
+// Tile choice of the LDS-DMA kernel. Large problems (at least 1024 blocks of 256 x 128): 256 x 256 blocks of 8 waves
+// at one workgroup per CU, a third less LDS-DMA traffic per MFMA than two 256 x 128 workgroups of 4 waves (measured
+// in the layer's back-to-back step, interleaved on one box: 2 % faster at K = 3072, 6 % at K = 12288). Otherwise
+// 128 x 128 blocks at two per CU (17 % faster than one per CU at M = 4096, K = N = 3072), and 128 x 64 blocks when
+// even those are too few to fill the chip.
 inline bool big_tiles(const GemmArgs& a) {
   const int64_t tiles = (int64_t)((a.M + 127) / 128) * ((a.N + 255) / 256);
   return tiles >= 1024;
 }
-inline bool deep_k(const GemmArgs& a) { return a.K >= 8192; }
 // 128 x 128 blocks of the problem (the small-problem tile).
 inline int64_t small_blocks(const GemmArgs& a) { return (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128); }
 
@@ -736,10 +734,7 @@ int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
     if (small_blocks(a) < 512) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
     return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
   } else {
-    if (big_tiles(a)) {
-      if (deep_k(a)) return launch_dma<4, 2, 4, 1, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
-      return launch_dma<4, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
-    }
+    if (big_tiles(a)) return launch_dma<4, 2, 4, 1, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
     // fewer 128 x 128 blocks than half the CUs: 128 x 64 blocks (measured 1.3x faster at 80 blocks, even at 160)
     if (small_blocks(a) < 128) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
     return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
@@ -834,8 +829,7 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
   args.a = a; args.w = w; args.c = c;
   args.lda = lda; args.ldw = ldw; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
-  if (big_tiles(args) && deep_k(args)) return launch_dma<4, 2, 4, 1, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
-  if (big_tiles(args)) return launch_dma<4, 2, 2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+  if (big_tiles(args)) return launch_dma<4, 2, 4, 1, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
   return launch_dma<2, 2, 2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
 }
 
@@ -860,8 +854,7 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
     if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 16)
       return set_error(PQ_EALIGN, "pq_int8_gemm_packed: int32 c must be 16-byte aligned with ldc %% 4 == 0");
     args.ldc = ldc;
-    if (big_tiles(args) && deep_k(args)) return launch_dma<4, 2, 4, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
-    if (big_tiles(args)) return launch_dma<4, 2, 2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+    if (big_tiles(args)) return launch_dma<4, 2, 4, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
     return launch_dma<2, 2, 2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
   }
   if (!s_row || !s_w) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null s_row / s_w");
