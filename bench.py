@@ -163,6 +163,7 @@ def main() -> int:
         cpu = cpu_baseline(cfg, lin, args.cpu_rows, args.cpu_iters)
     routing = route_bench(dev, not args.no_cpu) if cfg.routed else None
     launch = launch_bench(dev) if cfg.group else None
+    fold = fold_bench(dev, cfg) if cfg.name == "c1" else None
 
     res = {
         "metric": METRIC,
@@ -194,7 +195,7 @@ def main() -> int:
             "quantizer_alone": {"kernel": "quant_rows_packed", "us": round(qa_ms * 1e3, 1),
                                 "GBps": round(qa_gbs, 1), "frac_hbm": round(qa_gbs / HBM_PEAK_GBS, 4),
                                 "bytes": f"3 M K + 4 M{' + 4 M (gather list)' if rows is not None else ''}"},
-        } | ({"routing": routing} if routing is not None else {}) | ({"small_m_launch": launch} if launch else {}),
+        } | ({"routing": routing} if routing is not None else {}) | ({"small_m_launch": launch} if launch else {}) | ({"weight_fold": fold} if fold else {}),
         "roofline": {
             "bound": "mfma",
             "achieved": round(gemm_tops, 2),
@@ -210,6 +211,49 @@ def main() -> int:
     }
     print(json.dumps(res), flush=True)
     return 0
+
+
+def fold_bench(dev, cfg):
+    """The SVDQuant smoothing / shift fold of this layer's weight ([N, K] bf16, per-channel smooth and shift, bias) on
+    the GPU (pq_fold_weight), beside the reference's own torch-op sequence for it (deploy/run_flux_latency.py:219-239)
+    on the same GPU; 20 calls each after 3, queued behind a GPU sleep."""
+    import torch
+
+    from pyraquant_amd import weights
+
+    g = torch.Generator().manual_seed(1)
+    W = (torch.randn(cfg.N, cfg.K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    sm = (torch.rand(cfg.K, generator=g) + 0.5).to(dev)
+    sh = (torch.randn(cfg.K, generator=g) * 0.1).to(dev)
+    b = (torch.randn(cfg.N, generator=g) * 0.01).to(torch.bfloat16).to(dev)
+    out = torch.empty_like(W)
+
+    def torch_ops():
+        Wf = W.float() / sm.reshape(1, -1)
+        add = Wf @ sh.reshape(-1)
+        b2 = b.clone().add_(add.to(b.dtype))
+        out.copy_(Wf.to(W.dtype))
+        return b2
+
+    def timed(fn, n=20):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(50_000_000)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    us = timed(lambda: weights.fold_weight(W, sm, sh, b, out=out))
+    us_torch = timed(torch_ops)
+    nbytes = 4.0 * cfg.N * cfg.K
+    return {"shape": [cfg.N, cfg.K], "us": round(us, 1), "GBps": round(nbytes / us / 1e3, 1),
+            "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": "2 N K read + 2 N K written",
+            "reference_torch_ops_us": round(us_torch, 1)}
 
 
 def launch_bench(dev):

@@ -248,6 +248,22 @@ int pq_fuse_patches(const void* background, int64_t ldb, const void* patch_out, 
                     const int32_t* counts, const float* ramp, int64_t halo, float fusion_beta, int64_t H, int64_t W,
                     int64_t C, int32_t dtype, void* out, int64_t ldo, hipStream_t stream);
 
+/* ---- weight-side conversion ------------------------------------------------------------------------------ */
+
+/*
+ * Smoothing / shift fold of an SVDQuant package Linear, one pass over its 16-bit weight w [N, K] (row stride ldw):
+ *   Wf = (float)w / smooth                          (smooth: NULL, one fp32 scalar (n_smooth 1) or [K] fp32)
+ *   w_out[n, k] = Wf[n, k] rounded to dtype          (w_out may be w: in place; row stride ldo)
+ *   add[n] = sum_k Wf[n, k] * shift[k]  ([K] shift)  or  (sum_k Wf[n, k]) * shift[0]  (scalar shift)
+ *   bias_out[n] = round(bias_in[n] + round(add[n])) (bias_in NULL: round(add[n])), 16-bit dtype, may alias bias_in.
+ * Without shift bias_out may be NULL (the bias is unchanged). The shift sum is fp32 in an order of this kernel's
+ * own, so it agrees with torch's matmul to rounding. Replaces `_fold_one` (deploy/run_flux_latency.py:210-239) on
+ * the Int8Linear path, which then quantizes the folded weight (pq_quant_weight).
+ */
+int pq_fold_weight(const void* w, int32_t dtype, int64_t N, int64_t K, int64_t ldw, const float* smooth,
+                   int64_t n_smooth, const float* shift, int64_t n_shift, const void* bias_in, void* w_out,
+                   int64_t ldo, void* bias_out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -46,3 +46,19 @@ def int8_linear(x: torch.Tensor, w_int8: torch.Tensor, w_scale: torch.Tensor, bi
         t = x.to(lr_A.dtype) @ lr_A
         y.addmm_(t, lr_B)
     return y
+
+
+def fold_one(W: torch.Tensor, smooth=None, shift=None, bias=None):
+    """deploy/run_flux_latency.py:219-239 on the CPU: W [N, K] 16-bit, smooth / shift fp32 scalar or [K], bias 16-bit
+    or None. Returns (folded W in W's dtype, new bias or None), op for op as the reference writes it."""
+    dt = W.dtype
+    Wf = W.float()
+    if smooth is not None:
+        s = smooth.float()
+        Wf = Wf / s.reshape(()) if s.numel() == 1 else Wf / s.reshape(1, -1)
+    b = bias
+    if shift is not None:
+        sh = shift.float()
+        add = Wf.sum(dim=1) * sh.reshape(()) if sh.numel() == 1 else Wf @ sh.reshape(-1)
+        b = add.to(dt) if bias is None else bias.clone().add_(add.to(bias.dtype))
+    return Wf.to(dt), b

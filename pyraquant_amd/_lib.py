@@ -36,6 +36,7 @@ EXPORTS = (
     "pq_route_patches",
     "pq_gather_rows",
     "pq_fuse_patches",
+    "pq_fold_weight",
 )
 
 _p = ctypes.c_void_p
@@ -63,6 +64,7 @@ _SIGNATURES = {
     "pq_gather_rows": ([_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p], ctypes.c_int),
     "pq_fuse_patches": ([_p, _i64, _p, _i64, _p, _p, _p, _i64, ctypes.c_float, _i64, _i64, _i64, _i32, _p, _i64, _p],
                         ctypes.c_int),
+    "pq_fold_weight": ([_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p], ctypes.c_int),
 }
 
 _lib = None

@@ -462,6 +462,41 @@ def test_fusion_against_float64_blend():
         assert float(((out - ref).abs() / scale).max()) <= tol
 
 
+# ------------------------------------------------------------------------------------------- weight fold
+def test_fold_one_closed_forms():
+    """The smoothing / shift fold (deploy/run_flux_latency.py:219-239): no smooth and no shift is the identity;
+    a power-of-two smooth halves every normal weight exactly; a per-channel smooth of equal values equals the
+    scalar form; the shift term is within 16-bit rounding of the float64 dot product (per-channel and scalar);
+    a planted multiply-instead-of-divide fails."""
+    import torch
+
+    from oracle import torch_ref as T
+
+    g = torch.Generator().manual_seed(3)
+    for dt in (torch.bfloat16, torch.float16):
+        W = (torch.randn(64, 96, generator=g) * 0.05).to(dt)
+        b = (torch.randn(64, generator=g) * 0.01).to(dt)
+        w0, b0 = T.fold_one(W, None, None, b)
+        assert torch.equal(w0, W) and torch.equal(b0, b)
+        w2, _ = T.fold_one(W, torch.tensor(2.0), None, b)
+        normal = W.float().abs() > (2.0 ** -120 if dt == torch.bfloat16 else 2.0 ** -13)
+        assert torch.equal((w2.float() * 2)[normal], W.float()[normal])
+        ws, _ = T.fold_one(W, torch.tensor(1.7), None, b)
+        wv, _ = T.fold_one(W, torch.full((96,), 1.7), None, b)
+        assert torch.equal(ws, wv)
+        sm = torch.rand(96, generator=g) + 0.5
+        sh = torch.randn(96, generator=g) * 0.1
+        wf, bf = T.fold_one(W, sm, sh, b)
+        ref = b.double() + (W.double() / sm.double()) @ sh.double()
+        ulp = 2.0 ** -8 if dt == torch.bfloat16 else 2.0 ** -11
+        assert float(((bf.double() - ref).abs() / ref.abs().clamp_min(1e-3)).max()) <= 3 * ulp
+        _, bs = T.fold_one(W, sm, torch.tensor(0.3), None)
+        refs = (W.double() / sm.double()).sum(1) * 0.3
+        assert float(((bs.double() - refs).abs() / refs.abs().clamp_min(1e-3)).max()) <= 3 * ulp
+        wrong = (W.float() * sm.reshape(1, -1)).to(dt)
+        assert not torch.equal(wrong, wf)
+
+
 # ------------------------------------------------------------------------------------------- planted mistakes
 def test_planted_mistakes_are_caught(oracle):
     """Wrong variants of the oracle's arithmetic, computed here on the CPU, fail the checks above: round half
