@@ -11,7 +11,8 @@
 //
 // The kernel (gemm_dma_kernel). 2 x WMW wavefronts (WMW = 2 or 4 along m). A workgroup owns a BN x BM (n x m)
 // block, each wave a (BN/2) x (BM/WMW) part held as TI x TJ v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in
-// AGPRs). Large problems run 256 x 256 blocks of 8 waves at one workgroup per CU (128 accumulators per wave, two
+// VGPRs: the kernels name no AGPR, so the compiler selects the MFMA form whose C / D operands are VGPRs, and the
+// epilogue reads the accumulators in place, with no v_accvgpr_read copies). Large problems run 256 x 256 blocks of 8 waves at one workgroup per CU (128 accumulators per wave, two
 // waves per SIMD); small ones 128 x 128 blocks of 4 waves at two workgroups per CU, or 128 x 64 when the 128 x 128
 // blocks are too few to fill the chip.
 // K advances in stages of 64 bytes through a ring of NS LDS stages (5 x 32 KB for the 256 x 256 block) filled by
@@ -92,15 +93,6 @@ __device__ __forceinline__ v16f lr_mfma(v4i a, v4i b, v16f c) {
 // the per-row operands (s_row, the scatter row, the low-rank row t[m, :]) are issued by prefetch_rows() while the
 // last MFMAs run, and the per-column operands (s_w, bias, low-rank rows l2t[n, :]) of weight tile i + 1 are
 // issued before the tiles of weight tile i are computed. LRS = number of 16-wide low-rank slices held (0: none).
-// One int32 accumulator element read from its AGPR where it is used. Reading element by element keeps the
-// register allocator from copying every accumulator tile into VGPRs at once when the main loop ends (256
-// accumulators per lane do not fit next to the epilogue's operands and would spill).
-__device__ __forceinline__ int acc_read(int a) {
-  int v;
-  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
-  return v;
-}
-
 template <int TI, int TJ, int MODE, int LRS, int LRDT, int ODT, int CB = 2>
 struct Epilogue {
   // CB = 2: the column operands of weight tile i + 1 load while tile i is computed (one workgroup per CU);
@@ -190,12 +182,6 @@ struct Epilogue {
         for (int rs = 0; rs < RS; ++rs) tv[j][rs] = *reinterpret_cast<const v4i*>(rbuf + lr_off(ml, rs, khalf));
       }
     }
-    if constexpr (MODE == kModeChannel) {
-      // see run(): explicit MFMA -> v_accvgpr_read distance
-      __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
-      __builtin_amdgcn_sched_barrier(0);
-    }
     const int* orows = reinterpret_cast<const int*>(rbuf + 1024);
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
@@ -223,17 +209,23 @@ struct Epilogue {
           tile(acc[i][j], j, 0, has_bias, stage + (lane & 31) * kPitchL + (ii * 32 + 4 * khalf) * 2);
         }
         // staging -> global: 8 lanes x 16 bytes per 128-byte row piece, 8 rows per store instruction
+        // row addresses: one 32 x 32 -> 64-bit product per scattered row (ldc < 2^31), or the lane's first row plus a
+        // wave-uniform offset
         const int lr_ = lane >> 3, lc = lane & 7;
         const int n = nbase + ih * 64 + lc * 8;
         const bool nvalid = n < p.N;
+        const int ldc = (int)p.ldc;
+        uint16_t* const cn = static_cast<uint16_t*>(p.c) + n;
+        uint16_t* const cm = cn + (int64_t)(mbase + lr_) * ldc;
 #pragma unroll
         for (int s0 = 0; s0 < 32; s0 += 8) {
           const int row = s0 + lr_;
           const int m = mbase + j * 32 + row;
           const v4u v = *reinterpret_cast<const v4u*>(stage + row * kPitchL + lc * 16);
           if (nvalid && m < p.M) {
-            const int64_t o = p.out_row_idx ? (int64_t)orows[mloc + j * 32 + row] : (int64_t)m;
-            *reinterpret_cast<v4u*>(static_cast<uint16_t*>(p.c) + o * p.ldc + n) = v;
+            uint16_t* const dst = p.out_row_idx ? cn + (int64_t)orows[mloc + j * 32 + row] * ldc
+                                                : cm + (int64_t)(j * 32 + s0) * ldc;
+            *reinterpret_cast<v4u*>(dst) = v;
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -248,7 +240,7 @@ struct Epilogue {
     v16f y;
     if constexpr (MODE == kModeChannel) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) y[r] = (float)acc_read(a[r]) * (sr[j] * sc[c][r >> 2][r & 3]);
+      for (int r = 0; r < 16; ++r) y[r] = (float)a[r] * (sr[j] * sc[c][r >> 2][r & 3]);
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) y[r] = a[r] * sr[j];
@@ -287,13 +279,6 @@ struct Epilogue {
                                       uint8_t* stage) {
     const int khalf = lane >> 5;
     const bool has_bias = p.bias != nullptr;
-    if constexpr (MODE == kModeChannel) {
-      // The accumulators are read one element at a time by acc_read; the last MFMA into any of them is at least
-      // three MFMAs back, and 24 more wait states make the MFMA -> v_accvgpr_read distance explicit.
-      __builtin_amdgcn_sched_barrier(0);
-      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
-      __builtin_amdgcn_sched_barrier(0);
-    }
     if constexpr (MODE == kModeI32) {
 #pragma unroll
       for (int i = 0; i < TI; ++i) {
@@ -343,14 +328,17 @@ struct Epilogue {
       const int lr_ = lane / LPR, lc = lane % LPR;
       const int n = nbase + lc * 8;
       const bool nvalid = n < p.N;
+      const int ldc = (int)p.ldc;
+      uint16_t* const cn = static_cast<uint16_t*>(p.c) + n;
+      uint16_t* const cm = cn + (int64_t)(mbase + lr_) * ldc;
 #pragma unroll 4
       for (int s0 = 0; s0 < 32 * TJ; s0 += RPI) {
         const int row = s0 + lr_;
         const int m = mbase + row;
         const v4u v = *reinterpret_cast<const v4u*>(stage + row * kPitch + lc * 16);
         if (nvalid && m < p.M) {
-          const int64_t o = p.out_row_idx ? (int64_t)srow[row] : (int64_t)m;
-          *reinterpret_cast<v4u*>(static_cast<uint16_t*>(p.c) + o * p.ldc + n) = v;
+          uint16_t* const dst = p.out_row_idx ? cn + (int64_t)srow[row] * ldc : cm + (int64_t)s0 * ldc;
+          *reinterpret_cast<v4u*>(dst) = v;
         }
       }
     }
@@ -571,7 +559,7 @@ void gemm_dma_kernel(const GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < TJ; ++j) f[TI + j] = *reinterpret_cast<const v4i*>(sb + fa_off + j * 32 * kBKd + c);
   };
-  // Per-channel / int32: MFMA accumulation in AGPRs. Group-32: substep s of stage kt is K group g = 2 kt + s; its
+  // Per-channel / int32: MFMA accumulation in VGPRs. Group-32: substep s of stage kt is K group g = 2 kt + s; its
   // int32 partial is converted and fma'd with s_w[g, n] into the fp32 accumulator, groups in order (deploy
   // semantics: pyraquant/quantizers_weight.py:96-109). Lane element r of tile i holds row
   // n = wn BN / 2 + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4.
@@ -802,6 +790,7 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
   if (group != 0 && group != 32) return set_error(PQ_ESHAPE, "pq_int8_gemm: group must be 0 or 32, got %lld", (long long)group);
   if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 8)
     return set_error(PQ_EALIGN, "pq_int8_gemm: c must be 8-byte aligned with ldc >= N, ldc %% 4 == 0");
+  if (ldc > 0x7fffffffLL) return set_error(PQ_ESHAPE, "pq_int8_gemm: ldc %lld is 2^31 or more", (long long)ldc);
   if ((uintptr_t)s_w % 16 || (bias && (uintptr_t)bias % 16))
     return set_error(PQ_EALIGN, "pq_int8_gemm: s_w and bias must be 16-byte aligned");
   const bool has_lr = (t != nullptr) || (l2t != nullptr);
@@ -830,6 +819,7 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
   if (!c) return set_error(PQ_EINVAL, "pq_int8_gemm_i32: null c");
   if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 16)
     return set_error(PQ_EALIGN, "pq_int8_gemm_i32: c must be 16-byte aligned with ldc %% 4 == 0");
+  if (ldc > 0x7fffffffLL) return set_error(PQ_ESHAPE, "pq_int8_gemm_i32: ldc %lld is 2^31 or more", (long long)ldc);
   GemmArgs args{};
   args.a = a; args.w = w; args.c = c;
   args.lda = lda; args.ldw = ldw; args.ldc = ldc;
@@ -858,6 +848,7 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
   if (out_dtype == PQ_I32) {
     if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 16)
       return set_error(PQ_EALIGN, "pq_int8_gemm_packed: int32 c must be 16-byte aligned with ldc %% 4 == 0");
+    if (ldc > 0x7fffffffLL) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: ldc %lld is 2^31 or more", (long long)ldc);
     args.ldc = ldc;
     if (big_tiles(args)) return launch_dma<4, 2, 4, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
     return launch_dma<2, 2, 2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
@@ -867,6 +858,7 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
     return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: group must be 0 or 32, got %lld", (long long)group);
   if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 8)
     return set_error(PQ_EALIGN, "pq_int8_gemm_packed: c must be 8-byte aligned with ldc >= N, ldc %% 4 == 0");
+  if (ldc > 0x7fffffffLL) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: ldc %lld is 2^31 or more", (long long)ldc);
   if ((uintptr_t)s_w % 16 || (bias && (uintptr_t)bias % 16))
     return set_error(PQ_EALIGN, "pq_int8_gemm_packed: s_w and bias must be 16-byte aligned");
   const bool has_lr = (t != nullptr) || (l2t != nullptr);
