@@ -394,37 +394,39 @@ __global__ __launch_bounds__(256) void lowrank_down_dma_kernel(
 // ---- fused quantizer + low-rank down-projection (one read of x) ----------------------------------------------
 // pq_quant_rows_packed and pq_lowrank_down (R = 32) in one pass: deploy/int8_exec.py:390-391 computes
 // t = x @ lr_A and quant_rows(x) from the same x, and both need every element of a row.
-// One workgroup of 4 waves per CU, persistent over batches of 16 rows. A batch is brought into LDS by LDS-DMA in
+// One workgroup of W waves per CU, persistent over batches of 16 rows. A batch is brought into LDS by LDS-DMA in
 // 1 KB row-contiguous pieces (the DRAM-friendly pattern of the row-per-wave quantizer), then every wave reads its
-// K quarter [w K / 4, (w + 1) K / 4) of the 16 rows into registers (lane: row l % 16, K group l / 16), the DMA of the
+// K slice [w K / W, (w + 1) K / W) of the 16 rows into registers (lane: row l % 16, K group l / 16), the DMA of the
 // next batch is issued into the freed buffer, and the wave works from registers:
-//   absmax over the quarter -> LDS -> the row scale (the same IEEE steps as quant_rows_vec_kernel); codes from the
+//   absmax over the slice -> LDS -> the row scale (the same IEEE steps as quant_rows_vec_kernel); codes from the
 //   registers (quant_chunk), each wave storing whole 16-row x 64-byte packed K64 blocks;
-//   t partial = the quarter of x . l1t by v_mfma_f32_16x16x32, whose l1t slice stays in registers for the whole
-//   kernel -> LDS -> t = ((p0 + p1) + p2) + p3 in fp32, rounded to the 16-bit type.
-// K assignment inside the 64-wide K block c of a quarter (MFMA steps 2c and 2c + 1): lane group g covers
+//   t partial = the slice of x . l1t by v_mfma_f32_16x16x32, whose l1t slice stays in registers for the whole
+//   kernel -> LDS -> t = (..((p0 + p1) + p2) ..) + p(W-1) in fp32, rounded to the 16-bit type.
+// W = 16 where K allows it (K % 1024 == 0), else 8, else 4: the batch's work is spread over more waves while the
+// single LDS batch buffer (the memory pipeline) stays the same (c1: 143 -> 130 us from W = 4 to 16).
+// K assignment inside the 64-wide K block c of a slice (MFMA steps 2c and 2c + 1): lane group g covers
 // K [64 c + 16 g, +16), 8 values per step. Both MFMA operands use it, so each step contracts 32 distinct K; the
 // 16 codes a lane produces per block are chunk g of its row's 64-byte segment.
-template <int DT, int NC>   // NC: 64-wide K blocks per wave, K = 256 NC
-__global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
+template <int DT, int NC, int W>   // W waves, NC: 64-wide K blocks per wave, K = 64 W NC
+__global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int64_t M, const int32_t* __restrict__ row_idx,
     const uint16_t* __restrict__ l1t, int8_t* __restrict__ qp, float* __restrict__ s, uint16_t* __restrict__ t,
     int64_t ldt, int nbatch) {
-  constexpr int K = 256 * NC, R = 32, NS = 2 * NC;
+  constexpr int K = 64 * W * NC, R = 32, NS = 2 * NC;
   constexpr int CHUNKS = (2 * K + 1023) / 1024;      // 1 KB DMA pieces per row
   constexpr int PITCH = CHUNKS * 1024 + 64;          // LDS row pitch (+64 bytes: rows start 16 banks apart)
   __shared__ __attribute__((aligned(1024))) uint8_t xs[16 * PITCH];
-  __shared__ uint32_t amax_l[4][16];
-  __shared__ __attribute__((aligned(16))) float red[4][16][R];
+  __shared__ uint32_t amax_l[W][16];
+  __shared__ __attribute__((aligned(16))) float red[W][16][R];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int k0 = wave * (K / 4);
+  const int k0 = wave * (K / W);
   const int G = gridDim.x;
   const __amdgpu_buffer_rsrc_t rs_x =
       __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, (int)(x_rows * ldx * 2), kBufferWord3);
 
-  // l1t fragments of this wave's quarter: lf[h][2 c + e] = l1t[16 h + r][k0 + 64 c + 16 g + 8 e .. + 8]
+  // l1t fragments of this wave's slice: lf[h][2 c + e] = l1t[16 h + r][k0 + 64 c + 16 g + 8 e .. + 8]
   v4u lf[2][NS];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
@@ -433,17 +435,18 @@ __global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
       lf[h][i] = *reinterpret_cast<const v4u*>(l1t + (int64_t)(16 * h + r) * K + k0 + 64 * (i >> 1) + 16 * g +
                                                8 * (i & 1));
 
-  // DMA of batch b: wave w copies rows 4 w .. 4 w + 3, CHUNKS pieces each (rows past M: out of range, zeros).
+  // DMA of batch b: wave w copies rows (16 / W) w .. + 16 / W - 1, CHUNKS pieces each (rows past M: out of range,
+  // zeros).
   // Source rows come from uniform (scalar) reads of the gather list, so no vector load joins the vmcnt queue.
   auto dma = [&](int b) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t m = (int64_t)b * 16 + wave * 4 + j;
+    for (int j = 0; j < 16 / W; ++j) {
+      const int64_t m = (int64_t)b * 16 + wave * (16 / W) + j;
       int off = kOOB;
       if (m < M) off = (int)((row_idx ? (int64_t)row_idx[m] : m) * ldx * 2);
 #pragma unroll
       for (int c = 0; c < CHUNKS; ++c)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (lds_void_t*)(xs + (wave * 4 + j) * PITCH + c * 1024), 16,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (lds_void_t*)(xs + (wave * (16 / W) + j) * PITCH + c * 1024), 16,
                                                  off + c * 1024 + lane * 16, 0, 0, 0);
     }
   };
@@ -464,7 +467,7 @@ __global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
     dma(b + G < nbatch ? b + G : nbatch);
 
     const int64_t m = (int64_t)b * 16 + r;
-    // absmax: magnitude bits, packed u16 max, then the 4 lanes of the row, then the 4 quarters
+    // absmax: magnitude bits, packed u16 max, then the 4 lanes of the row, then the W slices
     us2 mx2 = {0, 0};
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
@@ -480,7 +483,7 @@ __global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
       mx = mx > o ? mx : o;
     }
     if (g == 0) amax_l[wave][r] = mx;
-    // low rank: partial t over the quarter (independent of the scale)
+    // low rank: partial t over the slice (independent of the scale)
     v4f acc[2] = {v4f{}, v4f{}};
 #pragma unroll
     for (int i = 0; i < NS; ++i)
@@ -499,11 +502,11 @@ __global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
     __builtin_amdgcn_sched_barrier(0);
     uint32_t am = amax_l[0][r];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) am = am > amax_l[w][r] ? am : amax_l[w][r];
+    for (int w = 1; w < W; ++w) am = am > amax_l[w][r] ? am : amax_l[w][r];
     const float a = fmaxf(lo16_to_f32<DT>(am), 1e-8f);
     const float sc = __fdiv_rn(a, 127.0f);
     const float rc = __fdiv_rn(1.0f, sc);
-    // codes: block c of the quarter, chunk g of row m (padding rows past M quantize zeros to zero codes)
+    // codes: block c of the slice, chunk g of row m (padding rows past M quantize zeros to zero codes)
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const v2u lo = quant_chunk<DT>(xv[2 * c], sc, rc);
@@ -518,11 +521,15 @@ __global__ __launch_bounds__(256, 1) void quant_lowrank_kernel(
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();   // red complete
     __builtin_amdgcn_sched_barrier(0);
-    {
+    if (tid < 256) {
       const int mr = tid >> 4, rr = (tid & 15) * 2;
       const int64_t mo = (int64_t)b * 16 + mr;
-      const float v0 = ((red[0][mr][rr] + red[1][mr][rr]) + red[2][mr][rr]) + red[3][mr][rr];
-      const float v1 = ((red[0][mr][rr + 1] + red[1][mr][rr + 1]) + red[2][mr][rr + 1]) + red[3][mr][rr + 1];
+      float v0 = red[0][mr][rr], v1 = red[0][mr][rr + 1];
+#pragma unroll
+      for (int w = 1; w < W; ++w) {
+        v0 = v0 + red[w][mr][rr];
+        v1 = v1 + red[w][mr][rr + 1];
+      }
       if (mo < M) *reinterpret_cast<uint32_t*>(t + mo * ldt + rr) = pack2<DT>(v0, v1);
     }
   }
@@ -668,18 +675,21 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
     return pq_lowrank_down(x, x_dtype, M, K, ldx, x_rows, row_idx, l1t, R, t, ldt, stream);
   }
   const int nbatch = (int)((M + 15) / 16);
-  const dim3 block(256), grid((unsigned)std::min(nbatch, 256));
+  const dim3 grid((unsigned)std::min(nbatch, 256));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* lp = static_cast<const uint16_t*>(l1t);
   uint16_t* tp = static_cast<uint16_t*>(t);
-#define PQ_QLCASE(D, NC)                                                                                     \
+  // nc = K / 256; W = 16 waves when nc % 4 == 0, 8 when nc % 2 == 0, else 4
+#define PQ_QLCASE(D, NC, W)                                                                                  \
   if (x_dtype == D && nc == NC) {                                                                           \
-    hipLaunchKernelGGL((quant_lowrank_kernel<D, NC>), grid, block, 0, stream, xp, ldx, x_rows, M, row_idx, lp, \
-                       qp, s, tp, ldt, nbatch);                                                             \
+    hipLaunchKernelGGL((quant_lowrank_kernel<D, NC * 4 / W, W>), grid, dim3(64 * W), 0, stream, xp, ldx, x_rows, \
+                       M, row_idx, lp, qp, s, tp, ldt, nbatch);                                             \
     return check_launch("quant_rows_lowrank");                                                              \
   }
-  PQ_QLCASE(PQ_BF16, 4) PQ_QLCASE(PQ_BF16, 5) PQ_QLCASE(PQ_BF16, 8) PQ_QLCASE(PQ_BF16, 10) PQ_QLCASE(PQ_BF16, 12)
-  PQ_QLCASE(PQ_F16, 4) PQ_QLCASE(PQ_F16, 5) PQ_QLCASE(PQ_F16, 8) PQ_QLCASE(PQ_F16, 10) PQ_QLCASE(PQ_F16, 12)
+  PQ_QLCASE(PQ_BF16, 4, 16) PQ_QLCASE(PQ_BF16, 5, 4) PQ_QLCASE(PQ_BF16, 8, 16) PQ_QLCASE(PQ_BF16, 10, 8)
+  PQ_QLCASE(PQ_BF16, 12, 16)
+  PQ_QLCASE(PQ_F16, 4, 16) PQ_QLCASE(PQ_F16, 5, 4) PQ_QLCASE(PQ_F16, 8, 16) PQ_QLCASE(PQ_F16, 10, 8)
+  PQ_QLCASE(PQ_F16, 12, 16)
 #undef PQ_QLCASE
   return set_error(PQ_ESHAPE, "pq_quant_rows_lowrank: unsupported shape");
 }
