@@ -153,7 +153,7 @@ def test_int8linear_packed_path(oracle, cuda, cfg, M):
 
 @pytest.mark.parametrize("M,N,K", [(8191, 6464, 1280), (16400, 4160, 192)])
 def test_gemm_big_tile_path_ragged(oracle, cuda, M, N, K):
-    """Shapes with >= 1024 256 x 128 tiles take the two-workgroups-per-CU kernel; ragged M and N (tail tiles on
+    """Shapes with >= 1024 tiles of 256 x 128 take the 256 x 256 block of 8 waves; ragged M and N (tail tiles on
     both edges) stay exact there, row-major and packed, and the fused outputs agree bit for bit."""
     from pyraquant_amd import int8_exec as E
 
@@ -238,7 +238,7 @@ def test_gemm_packed_group32_lowrank_scatter(oracle, cuda, lr):
 
 @pytest.mark.parametrize("M,N,K,lr", [(4352, 12288, 3072, 0), (4352, 12288, 3072, 32), (2100, 9216, 1280, 0)])
 def test_gemm_big_tile_rowmajor_equals_packed_repeated(cuda, M, N, K, lr):
-    """256 x 128 tiles on row-major operands (the reference self-test's int8_gemm_fused shape) give the packed path's
+    """256 x 256 blocks on row-major operands (the reference self-test's int8_gemm_fused shape) give the packed path's
     bits on every call. The last ring stages carry the epilogue operands; each stage must issue its full DMA count
     for the ring's vmcnt waits, so a stage that issues fewer leaves the previous stage's last tiles racing."""
     from pyraquant_amd import int8_exec as E
@@ -256,6 +256,32 @@ def test_gemm_big_tile_rowmajor_equals_packed_repeated(cuda, M, N, K, lr):
     for _ in range(4):
         y = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, torch.bfloat16)
         assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("R", [16, 64])
+def test_gemm_big_tile_lowrank_ranks(oracle, cuda, R):
+    """Ranks 16 and 64 on the 256 x 256 block: rank 16 rides the ring's epilogue stages, rank 64's rows do not fit
+    them and take the register epilogue. Both stay within the tolerance of the oracle on sampled rows (ragged last
+    rows included), and the row-major and packed paths agree bit for bit."""
+    from pyraquant_amd import int8_exec as E
+
+    M, N, K = 4352 + 37, 12288, 1024
+    a, w = _codes(M, N, K, 5 * R, cuda)
+    g = torch.Generator().manual_seed(R)
+    s_row = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(cuda)
+    s_w = (torch.rand(N, generator=g) * 2e-4 + 1e-5).to(cuda)
+    bias = (torch.randn(N, generator=g) * 0.01).to(cuda)
+    t = (torch.randn(M, R, generator=g) * 0.5).to(torch.bfloat16).to(cuda)
+    l2t = (torch.randn(N, R, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    got = E.int8_gemm_packed(E.pack_k64(a), s_row, E.pack_k64(w), s_w, bias, M, N, K, torch.bfloat16, t=t, l2t=l2t)
+    ref = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, torch.bfloat16)
+    assert torch.equal(got, ref)
+    sample = torch.cat([torch.arange(M - 40, M), torch.randperm(M - 40, generator=g)[:24]]).sort().values.to(cuda)
+    acc = oracle.gemm_i32(a[sample].cpu().numpy(), w.cpu().numpy())
+    yo = oracle.epilogue_f32(acc, s_row[sample].cpu().numpy(), s_w.cpu().numpy(), bias.cpu().numpy(),
+                             bits(t[sample]), bits(l2t.t().contiguous()), 0)
+    mx, mean = rel_errors(oracle.to_f32(bits(got[sample]), 0), yo)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
 
 
 @pytest.mark.parametrize("packed", [False, True])
