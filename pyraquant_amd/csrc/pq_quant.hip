@@ -391,6 +391,11 @@ __global__ __launch_bounds__(256) void lowrank_down_dma_kernel(
   }
 }
 
+// Byte offset of output row m's source row in x (x_rows * ldx * 2 < 2^30), or kOOB past M (a DMA that loads nothing).
+__device__ __forceinline__ int row_byte_offset(int64_t m, int64_t M, const int32_t* __restrict__ row_idx, int64_t ldx) {
+  return m < M ? (int)((row_idx ? (int64_t)row_idx[m] : m) * ldx * 2) : kOOB;
+}
+
 // ---- fused quantizer + low-rank down-projection (one read of x) ----------------------------------------------
 // pq_quant_rows_packed and pq_lowrank_down (R = 32) in one pass: deploy/int8_exec.py:390-391 computes
 // t = x @ lr_A and quant_rows(x) from the same x, and both need every element of a row.
@@ -438,12 +443,16 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
   // DMA of batch b: wave w copies rows (16 / W) w .. + 16 / W - 1, CHUNKS pieces each (rows past M: out of range,
   // zeros).
   // Source rows come from uniform (scalar) reads of the gather list, so no vector load joins the vmcnt queue.
-  auto dma = [&](int b) {
+  // xoff[j]: byte offset of this wave's row j of the batch whose DMA is issued next (kOOB past M). The gather index
+  // is read one batch ahead of its DMA, so the scalar load completes under the previous batch's work instead of
+  // delaying the DMA issue.
+  int xoff[16 / W];
+  auto row_off = [&](int bb, int j) { return row_byte_offset((int64_t)bb * 16 + wave * (16 / W) + j, M, row_idx, ldx); };
+  auto dma = [&]() {
 #pragma unroll
     for (int j = 0; j < 16 / W; ++j) {
-      const int64_t m = (int64_t)b * 16 + wave * (16 / W) + j;
-      int off = kOOB;
-      if (m < M) off = (int)((row_idx ? (int64_t)row_idx[m] : m) * ldx * 2);
+      // (a local copy: with the captured array element as the builtin's operand, hipcc emitted no host stub)
+      const int off = xoff[j];
 #pragma unroll
       for (int c = 0; c < CHUNKS; ++c)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (lds_void_t*)(xs + (wave * (16 / W) + j) * PITCH + c * 1024), 16,
@@ -454,7 +463,11 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
   v4u xv[NS];
   const uint8_t* xrow = xs + r * PITCH + 2 * (k0 + 16 * g);
   int b = blockIdx.x;
-  dma(b);
+#pragma unroll
+  for (int j = 0; j < 16 / W; ++j) xoff[j] = row_off(b, j);
+  dma();
+#pragma unroll
+  for (int j = 0; j < 16 / W; ++j) xoff[j] = row_off(b + G, j);
   for (; b < nbatch; b += G) {
     // The DMA of batch b is followed by the previous batch's stores; loads and stores are not guaranteed to
     // retire in issue order relative to each other, so wait for everything.
@@ -464,7 +477,9 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
     for (int i = 0; i < NS; ++i) xv[i] = *reinterpret_cast<const v4u*>(xrow + 128 * (i >> 1) + 16 * (i & 1));
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS reads are done
     __syncthreads();                      // every wave's are: the buffer takes the next batch
-    dma(b + G < nbatch ? b + G : nbatch);
+    dma();   // batch b + G
+#pragma unroll
+    for (int j = 0; j < 16 / W; ++j) xoff[j] = row_off(b + 2 * G, j);
 
     const int64_t m = (int64_t)b * 16 + r;
     // absmax: magnitude bits, packed u16 max, then the 4 lanes of the row, then the W slices
