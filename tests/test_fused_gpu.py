@@ -3,8 +3,8 @@
 * packed codes and scales bit-identical to pq_quant_rows_packed on the same rows (which the quantizer tests pin
   against the oracle);
 * t within bf16 rounding of the float64 product and within the build's tolerance of the oracle's fp32 result;
-* shapes the fused kernel does not take (K outside its list, R != 32) give exactly what the two separate entry
-  points give.
+* shapes the fused kernel does not take (K = 4096 .. 15360, K outside its list, R != 32) run the two kernels: the
+  same bar, and exactly what the two separate entry points give.
 """
 import numpy as np
 import pytest
@@ -32,7 +32,9 @@ def _check_t(oracle, t, x_rows, l1, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,K", [(1, 3072), (16, 3072), (17, 3072), (1000, 1280), (4099, 3072), (300, 2048),
-                                 (65, 2560), (33, 1024), (20000, 3072)])
+                                 (65, 2560), (33, 1024), (20000, 3072),
+                                 (1, 12288), (7, 12288), (1001, 12288), (37, 4096), (100, 5120), (50, 6144),
+                                 (23, 15360), (9000, 12288)])
 def test_quant_rows_lowrank_fused(oracle, cuda, dtype, M, K):
     from pyraquant_amd import int8_exec as E
     from pyraquant_amd.workloads import make_x
@@ -70,7 +72,7 @@ def test_quant_rows_lowrank_gather_view(oracle, cuda):
     _check_t(oracle, t, x.cpu()[idx.long()], l1, torch.bfloat16)
 
 
-@pytest.mark.parametrize("M,K,R", [(100, 12288, 32), (70, 640, 32), (300, 3072, 64)])
+@pytest.mark.parametrize("M,K,R", [(100, 12288, 32), (70, 640, 32), (300, 3072, 64), (40, 12288, 64)])
 def test_quant_rows_lowrank_fallback(cuda, M, K, R):
     """Shapes outside the fused kernel's set run the two kernels: identical to calling them one after the other."""
     from pyraquant_amd import int8_exec as E
@@ -82,6 +84,26 @@ def test_quant_rows_lowrank_fallback(cuda, M, K, R):
     qr, sr = E.quant_rows_packed(x)
     assert torch.equal(qp, qr) and torch.equal(s, sr)
     assert torch.equal(t, E.lowrank_down(x, l1t))
+
+
+def test_quant_rows_lowrank_wide_gather_view(oracle, cuda):
+    """K = 12288 (the two-kernel path) through a gather with duplicates and a row-slice view (ldx = K + 512): codes
+    and scales bit-identical to the packed quantizer's, t within bf16 rounding of the float64 product."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    rows, K, M = 600, 12288, 333
+    base = make_x(rows, K + 512, seed=9).to(cuda)
+    x = base[:, 512:]
+    g = torch.Generator().manual_seed(4)
+    idx = torch.randint(0, rows, (M,), generator=g, dtype=torch.int32)
+    idx[:3] = torch.tensor([rows - 1, 0, 0], dtype=torch.int32)
+    l1 = _l1(K, 32, torch.bfloat16, 13)
+    qp, s, t = E.quant_rows_lowrank(x, l1.t().contiguous().to(cuda), idx.to(cuda))
+    qr, sr = E.quant_rows_packed(x, idx.to(cuda))
+    assert torch.equal(qp, qr)
+    assert torch.equal(s, sr)
+    _check_t(oracle, t, x.cpu()[idx.long()], l1, torch.bfloat16)
 
 
 def test_int8linear_uses_fused_pass(oracle, cuda):
