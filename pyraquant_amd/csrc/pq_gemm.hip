@@ -332,6 +332,7 @@ struct Epilogue {
       // staging rows -> global: instruction s stores rows 16 s / TI + lane / (4 TI), 16 bytes per lane
       constexpr int LPR = 4 * TI;          // lanes per row
       constexpr int RPI = 64 / LPR;        // rows per store instruction
+      static_assert(64 % LPR == 0 && (32 * TJ) % RPI == 0, "whole rows per store instruction");
       const int lr_ = lane / LPR, lc = lane % LPR;
       const int n = nbase + lc * 8;
       const bool nvalid = n < p.N;
