@@ -258,29 +258,30 @@ def test_gemm_big_tile_rowmajor_equals_packed_repeated(cuda, M, N, K, lr):
         assert torch.equal(y, ref)
 
 
-@pytest.mark.parametrize("R", [16, 64])
-def test_gemm_big_tile_lowrank_ranks(oracle, cuda, R):
-    """Ranks 16 and 64 on the 256 x 256 block: rank 16 rides the ring's epilogue stages, rank 64's rows do not fit
-    them and take the register epilogue. Both stay within the tolerance of the oracle on sampled rows (ragged last
-    rows included), and the row-major and packed paths agree bit for bit."""
+@pytest.mark.parametrize("R,dt", [(16, torch.bfloat16), (32, torch.float16), (64, torch.bfloat16)])
+def test_gemm_big_tile_lowrank_ranks(oracle, cuda, R, dt):
+    """Ranks 16, 32 (fp16) and 64 on the 256 x 256 block: ranks 16 and 32 ride the ring's epilogue stages, rank 64's
+    rows do not fit them and take the register epilogue. All stay within the tolerance of the oracle on sampled rows
+    (ragged last rows included), and the row-major and packed paths agree bit for bit."""
     from pyraquant_amd import int8_exec as E
 
     M, N, K = 4352 + 37, 12288, 1024
+    code = dcode(dt)
     a, w = _codes(M, N, K, 5 * R, cuda)
     g = torch.Generator().manual_seed(R)
     s_row = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(cuda)
     s_w = (torch.rand(N, generator=g) * 2e-4 + 1e-5).to(cuda)
     bias = (torch.randn(N, generator=g) * 0.01).to(cuda)
-    t = (torch.randn(M, R, generator=g) * 0.5).to(torch.bfloat16).to(cuda)
-    l2t = (torch.randn(N, R, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
-    got = E.int8_gemm_packed(E.pack_k64(a), s_row, E.pack_k64(w), s_w, bias, M, N, K, torch.bfloat16, t=t, l2t=l2t)
-    ref = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, torch.bfloat16)
+    t = (torch.randn(M, R, generator=g) * 0.5).to(dt).to(cuda)
+    l2t = (torch.randn(N, R, generator=g) * 0.02).to(dt).to(cuda)
+    got = E.int8_gemm_packed(E.pack_k64(a), s_row, E.pack_k64(w), s_w, bias, M, N, K, dt, t=t, l2t=l2t)
+    ref = E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, dt)
     assert torch.equal(got, ref)
     sample = torch.cat([torch.arange(M - 40, M), torch.randperm(M - 40, generator=g)[:24]]).sort().values.to(cuda)
     acc = oracle.gemm_i32(a[sample].cpu().numpy(), w.cpu().numpy())
     yo = oracle.epilogue_f32(acc, s_row[sample].cpu().numpy(), s_w.cpu().numpy(), bias.cpu().numpy(),
-                             bits(t[sample]), bits(l2t.t().contiguous()), 0)
-    mx, mean = rel_errors(oracle.to_f32(bits(got[sample]), 0), yo)
+                             bits(t[sample]), bits(l2t.t().contiguous()), code)
+    mx, mean = rel_errors(oracle.to_f32(bits(got[sample]), code), yo)
     assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
 
 
