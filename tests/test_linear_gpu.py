@@ -275,3 +275,76 @@ def test_int8linear_graph_replay(cuda):
     g.replay()
     torch.cuda.synchronize()
     assert torch.equal(static_y, b(a(static_x)))
+
+
+class _FluxLike(torch.nn.Module):
+    """Module names as in FLUX's transformer: embedders, adaLN norms and proj_out stay bf16, token Linears convert."""
+
+    def __init__(self):
+        super().__init__()
+        L = lambda k, n: torch.nn.Linear(k, n, dtype=torch.bfloat16)   # noqa: E731
+        self.x_embedder = L(64, 128)
+        self.proj_out = L(128, 64)
+        self.transformer_blocks = torch.nn.ModuleList([torch.nn.Module()])
+        blk = self.transformer_blocks[0]
+        blk.attn = torch.nn.Module()
+        blk.attn.to_q = L(128, 128)
+        blk.norm1 = torch.nn.Module()
+        blk.norm1.linear = L(128, 768)
+        blk.ff = torch.nn.Module()
+        blk.ff.proj = L(128, 512)
+
+
+def test_module_conversion_and_warmup(cuda):
+    """convert_linears_to_int8 with the reference's default whitelist (deploy/int8_exec.py:415-445): the token
+    Linears become Int8Linear, whose outputs equal a directly built Int8Linear's; embedders, adaLN and proj_out stay
+    bf16; the statistics dict carries the reference's keys. warm_kernels runs every FLUX shape. The SDXL twins
+    (deploy/run_sdxl_latency.py:159-298) convert with their fp16 whitelist, per channel and group-32, and the
+    direct-launch helpers give the general wrappers' bits."""
+    import copy
+
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd import sdxl
+
+    m = _FluxLike().to(cuda)
+    ref_q = copy.deepcopy(m.transformer_blocks[0].attn.to_q)
+    rep = E.convert_linears_to_int8(m, device=cuda)
+    assert set(rep) == {"n_int8_linear", "n_bf16_linear_kept", "params_int8", "params_bf16_linear_kept",
+                        "bf16_kept_names", "int8_weight_gib", "bf16_equiv_gib"}
+    assert rep["n_int8_linear"] == 2 and rep["n_bf16_linear_kept"] == 3
+    assert sorted(rep["bf16_kept_names"]) == ["proj_out", "transformer_blocks.0.norm1.linear", "x_embedder"]
+    assert rep["params_int8"] == 128 * 128 + 128 * 512
+    blk = m.transformer_blocks[0]
+    assert isinstance(blk.attn.to_q, E.Int8Linear) and isinstance(blk.ff.proj, E.Int8Linear)
+    assert type(blk.norm1.linear) is torch.nn.Linear and type(m.x_embedder) is torch.nn.Linear
+    x = torch.randn(50, 128, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(cuda)
+    with torch.no_grad():
+        assert torch.equal(blk.attn.to_q(x), E.Int8Linear(ref_q, device=cuda)(x))
+    E.warm_kernels(device=cuda)
+
+    u = torch.nn.Module()
+    u.time_embedding = torch.nn.Module()
+    u.time_embedding.linear_1 = torch.nn.Linear(320, 1280, dtype=torch.float16)
+    u.down = torch.nn.Module()
+    u.down.to_q = torch.nn.Linear(640, 640, dtype=torch.float16)
+    u.down.ff = torch.nn.Linear(640, 2560, dtype=torch.float16)
+    u = u.to(cuda)
+    u32 = copy.deepcopy(u)
+    rep = sdxl.convert_unet_linears_to_int8(u, device=cuda)
+    assert rep["n_int8_linear"] == 2 and rep["fp16_kept_names"] == ["time_embedding.linear_1"]
+    assert rep["shapes_KxN"] == {"640x2560": 1, "640x640": 1}
+    rep32 = sdxl.convert_unet_linears_to_int8(u32, device=cuda, group_size=32)
+    assert isinstance(u32.down.ff, sdxl.SdxlInt8Linear) and u32.down.ff.group_size == 32 and rep32["n_int8_linear"] == 2
+    xs = torch.randn(154, 640, generator=torch.Generator().manual_seed(3)).to(torch.float16).to(cuda)
+    with torch.no_grad():
+        y, y32 = u.down.ff(xs), u32.down.ff(xs)
+    assert y.shape == y32.shape == (154, 2560) and torch.isfinite(y32.float()).all()
+    rel = float((y32.float() - y.float()).norm() / y.float().norm())
+    assert rel < 2e-2, rel                    # group-32 and per-channel RTN of the same weights
+    sdxl.warm_sdxl_kernels(device=cuda)
+    xq, sx = sdxl.fast_quant_rows(xs)
+    xq2, sx2 = E.quant_rows(xs)
+    assert torch.equal(xq, xq2) and torch.equal(sx, sx2)
+    q = u.down.to_q
+    assert torch.equal(sdxl.fast_gemm_fused(xq, sx, q.weight_int8, q.w_scale, q.bias, torch.float16),
+                       E.int8_gemm_fused(xq, sx, q.weight_int8, q.w_scale, q.bias, torch.float16))
