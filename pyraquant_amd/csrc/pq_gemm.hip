@@ -770,6 +770,9 @@ int dispatch_dtypes(GemmArgs& a, bool has_lr, int lr_dtype, int out_dtype, hipSt
   return set_error(PQ_EDTYPE, "pq_int8_gemm: unsupported output dtype %d", out_dtype);
 }
 
+// Largest row stride of t: 255 rows of it plus one 128-byte row stay below 2^31 bytes.
+constexpr int64_t kMaxLdt = 1LL << 22;
+
 int check_common(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, int64_t M, int64_t N, int64_t K,
                  const char* who) {
   if (M < 0 || N < 1 || K < 1) return set_error(PQ_ESHAPE, "%s: bad shape M=%lld N=%lld K=%lld", who, (long long)M, (long long)N, (long long)K);
@@ -812,6 +815,8 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
       return set_error(PQ_ESHAPE, "pq_int8_gemm: low-rank rank R=%lld must be 16, 32 or 64", (long long)R);
     if (ldt < R || ldt % 8 != 0 || (uintptr_t)t % 16 || (uintptr_t)l2t % 16)
       return set_error(PQ_EALIGN, "pq_int8_gemm: t, l2t must be 16-byte aligned with ldt %% 8 == 0");
+    // the epilogue addresses a tile's 256 rows of t with 32-bit buffer offsets
+    if (ldt > kMaxLdt) return set_error(PQ_ESHAPE, "pq_int8_gemm: ldt %lld exceeds %lld", (long long)ldt, (long long)kMaxLdt);
   }
   GemmArgs args{};
   args.a = a; args.w = w; args.s_row = s_row; args.s_w = s_w; args.bias = bias;
@@ -880,6 +885,8 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
       return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: low-rank rank R=%lld must be 16, 32 or 64", (long long)R);
     if (ldt < R || ldt % 8 != 0 || (uintptr_t)t % 16 || (uintptr_t)l2t % 16)
       return set_error(PQ_EALIGN, "pq_int8_gemm_packed: t, l2t must be 16-byte aligned with ldt %% 8 == 0");
+    // the epilogue addresses a tile's 256 rows of t with 32-bit buffer offsets
+    if (ldt > kMaxLdt) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: ldt %lld exceeds %lld", (long long)ldt, (long long)kMaxLdt);
   }
   args.s_row = s_row; args.s_w = s_w; args.bias = bias;
   args.t = static_cast<const uint16_t*>(t); args.l2t = static_cast<const uint16_t*>(l2t);

@@ -75,6 +75,9 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert gemm(ldc=1 << 31) == L.PQ_ESHAPE             # row offsets are 32 x 32-bit products
     assert gemm(t=p16, l2t=p16, R=24, ldt=24) == L.PQ_ESHAPE
     assert gemm(t=p16, l2t=nul, R=32, ldt=32) == L.PQ_EINVAL
+    assert gemm(t=p16, l2t=p16, R=32, ldt=(1 << 22) + 8) == L.PQ_ESHAPE   # t rows at 32-bit buffer offsets
+    assert lib.pq_int8_gemm_packed(p16, p16, p16, p16, 0, nul, p16, (1 << 22) + 8, p16, 32, 0, p16, 128, 0, nul,
+                                   8, 128, 128, nul) == L.PQ_ESHAPE
     assert gemm(od=5) == L.PQ_EDTYPE or gemm(od=5) == L.PQ_ELAUNCH
     assert gemm(M=0) == L.PQ_OK
     assert lib.pq_int8_gemm_i32(p16, 128, p16, 128, nul, 128, 8, 128, 128, nul) == L.PQ_EINVAL
