@@ -118,7 +118,7 @@ int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t 
  * form and the scatter have no reference kernel (weight semantics: pyraquant/quantizers_weight.py:96-109).
  * Requirements: K % 64 == 0, N % 64 == 0, M >= 1; a, w 16-byte aligned with lda, ldw % 16 == 0;
  * c 8-byte aligned with ldc % 4 == 0 and ldc < 2^31; t, l2t 16-byte aligned with ldt % 8 == 0, ldt <= 2^22,
- * R in {16, 32, 64};
+ * R in {16, 32, 64}; group 32 needs N * K < 2^33 (its scales are read at 32-bit buffer offsets);
  * lr_dtype and out_dtype are PQ_BF16 or PQ_F16; out_row_idx entries unique and in range.
  */
 int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,

@@ -803,6 +803,8 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
   if (M == 0) return PQ_OK;
   if (!s_row || !s_w || !c) return set_error(PQ_EINVAL, "pq_int8_gemm: null s_row / s_w / c");
   if (group != 0 && group != 32) return set_error(PQ_ESHAPE, "pq_int8_gemm: group must be 0 or 32, got %lld", (long long)group);
+  if (group == 32 && (K / 32) * N * 4 > kOOB - 4096)
+    return set_error(PQ_ESHAPE, "pq_int8_gemm: group-32 scales of %lld x %lld exceed the 32-bit buffer range", (long long)N, (long long)K);
   if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 8)
     return set_error(PQ_EALIGN, "pq_int8_gemm: c must be 8-byte aligned with ldc >= N, ldc %% 4 == 0");
   if (ldc > 0x7fffffffLL) return set_error(PQ_ESHAPE, "pq_int8_gemm: ldc %lld is 2^31 or more", (long long)ldc);
@@ -873,6 +875,8 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
   if (!s_row || !s_w) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null s_row / s_w");
   if (group != 0 && group != 32)
     return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: group must be 0 or 32, got %lld", (long long)group);
+  if (group == 32 && (K / 32) * N * 4 > kOOB - 4096)
+    return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: group-32 scales of %lld x %lld exceed the 32-bit buffer range", (long long)N, (long long)K);
   if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 8)
     return set_error(PQ_EALIGN, "pq_int8_gemm_packed: c must be 8-byte aligned with ldc >= N, ldc %% 4 == 0");
   if (ldc > 0x7fffffffLL) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: ldc %lld is 2^31 or more", (long long)ldc);

@@ -72,6 +72,8 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert gemm(N=96) == L.PQ_ESHAPE
     assert gemm(a=ctypes.c_void_p(8)) == L.PQ_EALIGN
     assert gemm(group=16) == L.PQ_ESHAPE
+    assert gemm(group=32, N=1 << 17, K=1 << 16, lda=1 << 16, ldw=1 << 16, ldc=1 << 17) == L.PQ_ESHAPE   # s_w > 1 GB
+    assert b"group-32 scales" in lib.pq_last_error()
     assert gemm(ldc=1 << 31) == L.PQ_ESHAPE             # row offsets are 32 x 32-bit products
     assert gemm(t=p16, l2t=p16, R=24, ldt=24) == L.PQ_ESHAPE
     assert gemm(t=p16, l2t=nul, R=32, ldt=32) == L.PQ_EINVAL
