@@ -12,6 +12,8 @@ namespace pq {
 // ---- C-ABI error reporting (thread-local text, returned status code) --------------------------------
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// A dispatch counts work-items in 32 bits per dimension: blocks * threads must stay below 2^32.
+int check_grid(int64_t blocks, int64_t threads, const char* what);
 
 // ---- vector types of the MFMA operands -----------------------------------------------------------------
 typedef int v4i __attribute__((ext_vector_type(4)));

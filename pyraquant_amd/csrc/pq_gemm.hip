@@ -689,11 +689,11 @@ void gemm_dma_kernel(const GemmArgs p) {
 }
 
 // ---- launchers ---------------------------------------------------------------------------------------------
-int grid_of(GemmArgs& a, int BM, int BN, dim3& grid) {
+int grid_of(GemmArgs& a, int BM, int BN, int threads, dim3& grid) {
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
   const int64_t nblocks = (int64_t)a.tiles_m * a.tiles_n;
-  if (nblocks > 0x7fffffff) return set_error(PQ_ESHAPE, "pq_int8_gemm: too many tiles");
+  if (const int st = check_grid(nblocks, threads, "pq_int8_gemm")) return st;
   grid = dim3((unsigned)nblocks);
   return PQ_OK;
 }
@@ -711,7 +711,7 @@ template <int TI, int TJ, int WMW, int OCC, bool PACKED, int MODE, int LRS, int 
 int launch_dma(GemmArgs& a, hipStream_t stream) {
   constexpr int NS = ring_stages<TI, TJ, WMW, OCC, MODE>();
   dim3 grid;
-  const int st = grid_of(a, 32 * TJ * WMW, 64 * TI, grid);
+  const int st = grid_of(a, 32 * TJ * WMW, 64 * TI, 128 * WMW, grid);
   if (st != PQ_OK) return st;
   hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, WMW, NS, OCC, PACKED, MODE, LRS, LRDT, ODT>), grid, dim3(128 * WMW), 0,
                      stream, a);

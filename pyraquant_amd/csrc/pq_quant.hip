@@ -181,6 +181,7 @@ int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t
                  float* s, hipStream_t stream) {
   const dim3 block(256);
   const int64_t rows = PACKED ? ((M + 15) & ~15LL) : M;
+  if (const int st = check_grid((rows + 3) / 4, 256, "quant_rows")) return st;
   const dim3 grid((unsigned)((rows + 3) / 4));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const bool vec = ((uintptr_t)x % 16 == 0) && (ldx % 8 == 0) && (K % 8 == 0) && ((uintptr_t)q % 8 == 0);
@@ -587,6 +588,13 @@ int set_error(int code, const char* fmt, ...) {
   return code;
 }
 
+int check_grid(int64_t blocks, int64_t threads, const char* what) {
+  if (blocks * threads > 0xffffffffLL)
+    return set_error(PQ_ESHAPE, "%s: %lld blocks of %lld threads exceed the 32-bit dispatch size", what,
+                     (long long)blocks, (long long)threads);
+  return PQ_OK;
+}
+
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(PQ_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
@@ -642,6 +650,7 @@ extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t 
   if ((uintptr_t)x % 16 || (uintptr_t)l1t % 16 || (uintptr_t)t % 16)
     return set_error(PQ_EALIGN, "pq_lowrank_down: x, l1t, t must be 16-byte aligned");
   if (dtype != PQ_BF16 && dtype != PQ_F16) return set_error(PQ_EDTYPE, "pq_lowrank_down: bad dtype %d", (int)dtype);
+  if (const int st = check_grid((M + 127) / 128, 256, "pq_lowrank_down")) return st;
   const dim3 block(256), grid((unsigned)((M + 127) / 128));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* lp = static_cast<const uint16_t*>(l1t);
@@ -720,6 +729,7 @@ extern "C" int pq_dequant_epilogue(const int32_t* acc, const float* s_row, const
   if ((uintptr_t)acc % 16 || (uintptr_t)s_col % 16 || (uintptr_t)c % 8 || (bias && (uintptr_t)bias % 16))
     return set_error(PQ_EALIGN, "pq_dequant_epilogue: misaligned operand");
   const int64_t groups = M * (N / 4);
+  if (const int st = check_grid((groups + 255) / 256, 256, "pq_dequant_epilogue")) return st;
   const dim3 block(256), grid((unsigned)((groups + 255) / 256));
   if (out_dtype == PQ_BF16) {
     hipLaunchKernelGGL((dequant_epilogue_kernel<PQ_BF16>), grid, block, 0, stream, acc, s_row, s_col, bias,
@@ -744,6 +754,7 @@ extern "C" int pq_quant_weight(const float* w, int64_t N, int64_t K, int64_t ldw
   if (K > (1LL << 30) || N > (1LL << 30)) return set_error(PQ_ESHAPE, "pq_quant_weight: shape too large");
   const int g = group ? (int)group : (int)K;
   const int64_t segs = N * (K / g);
+  if (const int st = check_grid((segs + 3) / 4, 256, "pq_quant_weight")) return st;
   hipLaunchKernelGGL(quant_weight_kernel, dim3((unsigned)((segs + 3) / 4)), dim3(256), 0, stream, w, ldw, (int)N,
                      (int)K, g, q, s);
   return check_launch("quant_weight");
@@ -756,6 +767,7 @@ extern "C" int pq_pack_k64(const int8_t* src, int64_t R, int64_t K, int64_t lds,
   if (lds < K || lds % 16 || (uintptr_t)src % 16 || (uintptr_t)dst % 16)
     return set_error(PQ_EALIGN, "pq_pack_k64: src / dst 16-byte aligned, lds %% 16 == 0 and lds >= K required");
   const int64_t nslots = ((R + 15) / 16) * (K / 64) * 64;
+  if (const int st = check_grid((nslots + 255) / 256, 256, "pq_pack_k64")) return st;
   hipLaunchKernelGGL(pack_k64_kernel, dim3((unsigned)((nslots + 255) / 256)), dim3(256), 0, stream, src, R,
                      (int)(K / 64), lds, dst, nslots);
   return check_launch("pack_k64");

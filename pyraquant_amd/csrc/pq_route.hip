@@ -488,6 +488,7 @@ extern "C" int pq_fuse_patches(const void* background, int64_t ldb, const void* 
   if (halo < 0 || halo > kMaxFuseHalo)
     return set_error(PQ_EINVAL, "pq_fuse_patches: halo %lld outside [0, %d]", (long long)halo, kMaxFuseHalo);
   const int64_t n = H * W * (C / 8);
+  if (const int st = check_grid((n + 255) / 256, 256, "pq_fuse_patches")) return st;
   const dim3 grid((unsigned)((n + 255) / 256));
   const size_t lds = sizeof(float) * (size_t)std::max<int64_t>(halo * (halo + 1), 1);
   if (dtype == PQ_BF16)

@@ -124,6 +124,7 @@ extern "C" int pq_fold_weight(const void* w, int32_t dtype, int64_t N, int64_t K
       (bias_out && (uintptr_t)bias_out % 2) || (smooth && (uintptr_t)smooth % 4) || (shift && (uintptr_t)shift % 4))
     return set_error(PQ_EALIGN, "pq_fold_weight: misaligned operand");
   if (dtype != PQ_BF16 && dtype != PQ_F16) return set_error(PQ_EDTYPE, "pq_fold_weight: dtype %d", dtype);
+  if (const int st = check_grid(N, 256, "pq_fold_weight")) return st;
   const dim3 grid((unsigned)N), block(256);
   const bool vec = K % 8 == 0 && ldw % 8 == 0 && ldo % 8 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)w_out % 16 == 0 &&
                    (!smooth || n_smooth == 1 || (uintptr_t)smooth % 16 == 0) &&

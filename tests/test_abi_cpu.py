@@ -87,6 +87,10 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert lib.pq_quant_weight(p16, 4, 64, 64, 48, p16, p16, nul) == L.PQ_ESHAPE
     assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, 8, nul, p16, 24, p16, 32, nul) == L.PQ_ESHAPE
     assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, 4, nul, p16, 32, p16, 32, nul) == L.PQ_ESHAPE   # x_rows < M
+    # grids beyond the 32-bit work-item count of one dispatch are refused before any launch
+    assert lib.pq_quant_rows(p16, 0, (1 << 26) + 64, 64, 64, nul, p16, p16, nul) == L.PQ_ESHAPE
+    assert b"32-bit dispatch" in lib.pq_last_error()
+    assert lib.pq_pack_k64(p16, 1 << 31, 64 * 1024, 64 * 1024, p16, nul) == L.PQ_ESHAPE
     assert lib.pq_dequant_epilogue(nul, nul, nul, nul, nul, 128, 0, 8, 128, nul) == L.PQ_EINVAL
     # routing geometry and fusion
     assert lib.pq_route_union_rows(nul, 16, 16, 16, 2, 256, 256, p16, p16, nul) == L.PQ_EINVAL
