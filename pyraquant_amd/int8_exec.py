@@ -112,9 +112,11 @@ def dequant_epilogue(acc: torch.Tensor, s_row: torch.Tensor, s_col: torch.Tensor
     assert acc.dtype == torch.int32 and acc.is_contiguous()
     _check_cuda(acc, s_row, s_col, bias)
     M, N = acc.shape
+    s_row, s_col = s_row.float().contiguous(), s_col.float().contiguous()
+    assert s_row.numel() >= M and s_col.numel() >= N, (s_row.numel(), s_col.numel(), M, N)
     out = torch.empty((M, N), dtype=out_dtype, device=acc.device)
     L = _lib.load()
-    _lib.check(L.pq_dequant_epilogue(_lib.ptr(acc), _lib.ptr(s_row.contiguous()), _lib.ptr(s_col.contiguous()),
+    _lib.check(L.pq_dequant_epilogue(_lib.ptr(acc), _lib.ptr(s_row), _lib.ptr(s_col),
                                      _lib.ptr(None if bias is None else bias.float().contiguous()), _lib.ptr(out), N,
                                      _lib.dtype_code(out_dtype), M, N, _lib.stream_of(acc.device)), "dequant_epilogue")
     return out
@@ -133,6 +135,7 @@ def _gemm(xq: torch.Tensor, s_row: torch.Tensor, w_int8: torch.Tensor, w_scale_k
     assert xq.stride(1) == 1 and w_int8.stride(1) == 1
     assert s_row.dtype == torch.float32 and s_row.is_contiguous() and s_row.numel() >= M
     assert w_scale_k.dtype == torch.float32 and w_scale_k.is_contiguous()
+    assert w_scale_k.numel() == (N * K // 32 if group else N), (tuple(w_scale_k.shape), N, K, group)
     if bias is not None:
         assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == N
     ori = _row_index(out_row_idx, xq.device)
@@ -146,6 +149,7 @@ def _gemm(xq: torch.Tensor, s_row: torch.Tensor, w_int8: torch.Tensor, w_scale_k
     lr_code, R, ldt = 0, 0, 0
     if t is not None:
         assert l2t is not None and t.dtype == l2t.dtype and t.stride(1) == 1 and l2t.is_contiguous()
+        assert t.dim() == 2 and t.shape[0] >= M, (tuple(t.shape), M)
         R = t.shape[1]
         assert l2t.shape == (N, R), (tuple(l2t.shape), (N, R))
         lr_code, ldt = _lib.dtype_code(t.dtype), t.stride(0)
@@ -298,6 +302,7 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
     lr_code, R, ldt = 0, 0, 0
     if t is not None:
         assert l2t is not None and t.dtype == l2t.dtype and t.stride(1) == 1 and l2t.is_contiguous()
+        assert t.dim() == 2 and t.shape[0] >= M, (tuple(t.shape), M)
         R = t.shape[1]
         assert l2t.shape == (N, R), (tuple(l2t.shape), (N, R))
         lr_code, ldt = _lib.dtype_code(t.dtype), t.stride(0)
