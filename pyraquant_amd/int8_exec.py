@@ -348,6 +348,20 @@ def quantize_weight(w: torch.Tensor, group_size: int = 0) -> Tuple[torch.Tensor,
 LOWRANK_A_ATTR = "_lowrank_A"
 LOWRANK_B_ATTR = "_lowrank_B"
 
+# Ranks the kernels take: the down-projection writes t in multiples of 32 columns (up to 128), the GEMM epilogue
+# holds 16, 32 or 64 of them. Other ranks run zero-padded (zero columns of lr_A / rows of lr_B add exact zeros);
+# above 64 the up-projection runs after the GEMM as an in-place addmm, the reference's unfused order
+# (deploy/int8_exec.py:394-407).
+_LR_DOWN_MAX = 128
+_LR_EPILOGUE_RANKS = (16, 32, 64)
+
+
+def _lowrank_widths(R: int) -> Tuple[int, int]:
+    """(columns of t the down-projection computes, rank the GEMM epilogue takes; 0 = after the GEMM)."""
+    r_down = (R + 31) // 32 * 32
+    r_epi = next((r for r in _LR_EPILOGUE_RANKS if r >= R), 0)
+    return (r_down if r_down <= _LR_DOWN_MAX else 0), r_epi
+
 
 class Int8Linear(nn.Module):
     """INT8 stand-in for nn.Linear (deploy/int8_exec.py:345-411): int8 weights (buffers) + per-token dynamic
@@ -392,10 +406,22 @@ class Int8Linear(nn.Module):
         if A is not None and B is not None:
             A = A.to(device) if device is not None else A
             B = B.to(device) if device is not None else B
+            assert A.dim() == 2 and B.dim() == 2 and A.shape[1] == B.shape[0], (tuple(A.shape), tuple(B.shape))
+            assert A.shape[0] == K and B.shape[1] == N, (tuple(A.shape), tuple(B.shape), K, N)
             self.register_buffer("lr_A", A.contiguous())
             self.register_buffer("lr_B", B.contiguous())
-            self.register_buffer("lr_At", A.t().contiguous())
-            self.register_buffer("lr_Bt", B.t().contiguous())
+            R = A.shape[1]
+            r_down, r_epi = _lowrank_widths(R)
+            # kernel copies: lr_At [r_down, K] and lr_Bt [N, r_epi], zero-padded past rank R
+            At = None
+            if r_down and A.dtype in (torch.bfloat16, torch.float16):
+                At = A.new_zeros((r_down, K))
+                At[:R] = A.t()
+            self.register_buffer("lr_At", At)
+            Bt = B.new_zeros((N, r_epi)) if r_epi else None
+            if Bt is not None:
+                Bt[:, :R] = B.t()
+            self.register_buffer("lr_Bt", Bt)
         else:
             self.lr_A = None
             self.lr_B = None
@@ -427,7 +453,10 @@ class Int8Linear(nn.Module):
         x2 = x.reshape(-1, K)
         if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
             return None
-        R = 0 if self.lr_At is None else self.lr_At.shape[0]
+        if self.lr_A is not None and (self.lr_At is None or self.lr_Bt is None):
+            return None
+        R = 0 if self.lr_At is None else self.lr_At.shape[0]          # columns of t
+        Re = 0 if self.lr_Bt is None else self.lr_Bt.shape[1]         # rank of the epilogue
         if R and (self.lr_At.dtype != dt or self.lr_Bt.dtype != dt):
             return None
         M = x2.shape[0]
@@ -451,7 +480,7 @@ class Int8Linear(nn.Module):
             _lib.check(st, what)
         st = L.pq_int8_gemm_packed(base, self.weight_packed.data_ptr(), base + s_off, self._scale_k().data_ptr(),
                                    self.group_size, None if self.bias is None else self.bias.data_ptr(),
-                                   base + t_off if R else None, R, self.lr_Bt.data_ptr() if R else None, R,
+                                   base + t_off if R else None, R, self.lr_Bt.data_ptr() if R else None, Re,
                                    code, out.data_ptr(), N, code, None, M, N, K, stream)
         if st:
             _lib.check(st, "int8_gemm_packed")
@@ -470,26 +499,55 @@ class Int8Linear(nn.Module):
         if x2.stride(1) != 1:
             x2 = x2.contiguous()
         t = None
-        fused = self.weight_packed is not None and self.lr_A is not None and x2.dtype == self.lr_A.dtype
+        fused = self.weight_packed is not None and self.lr_At is not None and x2.dtype == self.lr_A.dtype
         if fused:
             # quantizer and low-rank down-projection from one pass over x (deploy/int8_exec.py:390-391)
             xq, sx, t = quant_rows_lowrank(x2, self.lr_At, row_idx)
         elif self.lr_A is not None:
             xl = x2 if x2.dtype == self.lr_A.dtype else x2.to(self.lr_A.dtype)
-            t = lowrank_down(xl, self.lr_At, row_idx)
+            if self.lr_At is not None:
+                t = lowrank_down(xl, self.lr_At, row_idx)
+            else:   # a rank beyond the down-projection kernel's, or a 32-bit lr_A: torch's product, as the reference
+                t = (xl if row_idx is None else xl.index_select(0, row_idx.long())) @ self.lr_A
             if t.dtype != x2.dtype:
                 t = t.to(x2.dtype)
+        t_epi = None if t is None or self.lr_Bt is None else t[:, :self.lr_Bt.shape[1]]
+        if t is not None and t_epi is None:
+            return self._forward_lr_after(x2, shape, xq if fused else None, sx if fused else None, t, row_idx, out,
+                                          out_row_idx)
         if self.weight_packed is not None:
             if not fused:
                 xq, sx = quant_rows_packed(x2, row_idx)
             y = int8_gemm_packed(xq, sx, self.weight_packed, self._scale_k(), self.bias, sx.shape[0],
-                                 self.out_features, self.in_features, x2.dtype, t=t, l2t=self._lr_bt(x2.dtype),
+                                 self.out_features, self.in_features, x2.dtype, t=t_epi, l2t=self._lr_bt(x2.dtype),
                                  out=out, out_row_idx=out_row_idx, group=self.group_size)
         else:
             xq, sx = quant_rows(x2, row_idx)
-            y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, t,
+            y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, t_epi,
                       self._lr_bt(x2.dtype), x2.dtype, out, out_row_idx)
         if out is not None or row_idx is not None:
+            return y
+        return y.reshape(*shape[:-1], self.out_features)
+
+    def _forward_lr_after(self, x2, shape, xq, sx, t, row_idx, out, out_row_idx):
+        """Ranks above the epilogue's: the GEMM without the low-rank term, then y += t @ lr_B in place
+        (deploy/int8_exec.py:394-407), then the scatter into the canvas if one is given."""
+        if xq is None:
+            xq, sx = quant_rows_packed(x2, row_idx) if self.weight_packed is not None else quant_rows(x2, row_idx)
+        M = sx.shape[0]
+        if self.weight_packed is not None:
+            y = int8_gemm_packed(xq, sx, self.weight_packed, self._scale_k(), self.bias, M, self.out_features,
+                                 self.in_features, x2.dtype, group=self.group_size)
+        else:
+            y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, None, None, x2.dtype)
+        y.addmm_(t[:, :self.lr_A.shape[1]], self.lr_B.to(y.dtype))
+        if out is not None:
+            if out_row_idx is not None:
+                out.index_copy_(0, out_row_idx.long(), y)
+            else:
+                out[:M].copy_(y)
+            return out
+        if row_idx is not None:
             return y
         return y.reshape(*shape[:-1], self.out_features)
 

@@ -167,3 +167,13 @@ def test_whitelists():
         assert not is_bf16_whitelisted(n), n
     assert is_fp16_whitelisted_sdxl("time_embedding.linear_1") and is_fp16_whitelisted_sdxl("down.0.time_emb_proj")
     assert not is_fp16_whitelisted_sdxl("down_blocks.1.attentions.0.proj_in")
+
+
+def test_lowrank_widths():
+    """Rank -> (columns of t the down-projection computes, rank the GEMM epilogue takes; 0 = after the GEMM)."""
+    from pyraquant_amd.int8_exec import _lowrank_widths
+
+    expect = {1: (32, 16), 16: (32, 16), 17: (32, 32), 32: (32, 32), 33: (64, 64), 48: (64, 64), 64: (64, 64),
+              65: (96, 0), 96: (96, 0), 128: (128, 0), 129: (0, 0), 200: (0, 0)}
+    for r, w in expect.items():
+        assert _lowrank_widths(r) == w, (r, _lowrank_widths(r), w)

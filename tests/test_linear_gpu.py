@@ -75,6 +75,45 @@ def test_int8linear_flux(oracle, cuda, cfg, M):
     assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
 
 
+@pytest.mark.parametrize("K,R", [(1280, 8), (1280, 16), (640, 16), (3072, 48), (640, 96), (1280, 128), (640, 160)])
+def test_int8linear_any_rank(oracle, cuda, K, R):
+    """The reference's Int8Linear takes a low-rank branch of any rank (deploy/int8_exec.py:371-407). Ranks the
+    kernels do not take as they are run zero-padded, and above 64 with the up-projection after the GEMM (the
+    reference's unfused order). The output is within tolerance of the oracle, the direct path equals the general
+    path, and a routed call (gather + scatter into a canvas) matches the oracle's gathered rows."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    lin = make_linear(K, 640, R, True, seed=R)
+    q = E.Int8Linear(lin, device=cuda)
+    assert q.lr_A.shape == (K, R) and q.lr_B.shape == (R, 640)   # the reference's buffers keep their rank
+    x = make_x(300, K, torch.bfloat16, seed=R).to(cuda)
+    y = q(x)
+    o = _oracle_module(oracle, q, x)
+    mx, mean = rel_errors(oracle.to_f32(bits(y), 0), o["y"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    E.DIRECT_CALLS = False
+    try:
+        y2 = q(x)
+    finally:
+        E.DIRECT_CALLS = True
+    assert torch.equal(y, y2)
+
+    g = torch.Generator().manual_seed(R)
+    ri = torch.randperm(300, generator=g)[:77].to(torch.int32)
+    ori = torch.randperm(500, generator=g)[:77].to(torch.int32)
+    canvas = torch.randn(500, 640, generator=g).to(torch.bfloat16).to(cuda)
+    before = canvas.clone()
+    q(x, row_idx=ri.to(cuda), out=canvas, out_row_idx=ori.to(cuda))
+    o = _oracle_module(oracle, q, x, row_idx=ri)
+    rows = ori.long()
+    mx, mean = rel_errors(oracle.to_f32(bits(canvas[rows.to(cuda)]), 0), o["y"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    keep = torch.ones(500, dtype=torch.bool)
+    keep[rows] = False
+    assert torch.equal(canvas[keep.to(cuda)], before[keep.to(cuda)])
+
+
 def test_int8linear_3d_and_views(cuda):
     """Leading dims are flattened and restored; a 3-D input gives the same result as its 2-D view
     (deploy/int8_exec.py:530-531); a row-slice input needs no copy."""
