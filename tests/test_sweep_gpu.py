@@ -6,7 +6,7 @@ a routed call (gather of M rows of a larger x and a scatter into a larger canvas
   * weight codes / scales and activation codes / scales are bit-exact against the oracle
     (pyraquant/quantizers_weight.py:96-109, deploy/int8_exec.py:352-357, :508-509);
   * the layer output is within the build's tolerance of the oracle's fp32 result computed from the same codes
-    (deploy/int8_exec.py:382-393; order of the epilogue :303-309);
+    (deploy/int8_exec.py:382-393; order of the epilogue :303-309), and bit-exact when there is no low-rank term;
   * the direct call path gives the same bits as the general wrappers;
   * rows of a scatter canvas that the call does not name keep their contents.
 """
@@ -96,6 +96,8 @@ def test_int8linear_random_sweep(oracle, cuda, i):
 
     mx, mean = rel_errors(oracle.to_f32(bits(y), dcode(dt)), o["y"])
     assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    if not R:   # no low-rank sum: the epilogue runs the oracle's fp32 operations in its order, so the bits agree
+        assert np.array_equal(bits(y), o["out"])
 
     if c["routed"]:
         keep = torch.ones(M + 30, dtype=torch.bool)
