@@ -509,6 +509,8 @@ class Int8Linear(nn.Module):
                 t = lowrank_down(xl, self.lr_At, row_idx)
             else:   # a rank beyond the down-projection kernel's, or a 32-bit lr_A: torch's product, as the reference
                 t = (xl if row_idx is None else xl.index_select(0, row_idx.long())) @ self.lr_A
+                if self.lr_Bt is not None and t.shape[1] < self.lr_Bt.shape[1]:
+                    t = F.pad(t, (0, self.lr_Bt.shape[1] - t.shape[1]))   # zero columns, as the padded lr_At gives
             if t.dtype != x2.dtype:
                 t = t.to(x2.dtype)
         t_epi = None if t is None or self.lr_Bt is None else t[:, :self.lr_Bt.shape[1]]

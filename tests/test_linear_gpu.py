@@ -114,6 +114,25 @@ def test_int8linear_any_rank(oracle, cuda, K, R):
     assert torch.equal(canvas[keep.to(cuda)], before[keep.to(cuda)])
 
 
+def test_int8linear_fp32_lowrank(oracle, cuda):
+    """A 32-bit low-rank branch (rank 48): t from torch's fp32 product, zero-padded to the epilogue's rank 64,
+    rounded to the activation type with lr_B. Within tolerance of the oracle run on the 16-bit-rounded factors."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    lin = make_linear(1280, 640, 0, True, seed=5)
+    g = torch.Generator().manual_seed(5)
+    A, B = torch.randn(1280, 48, generator=g) * 0.02, torch.randn(48, 640, generator=g) * 0.02
+    q = E.Int8Linear(lin, device=cuda, lowrank=(A, B))
+    assert q.lr_At is None and q.lr_Bt.shape == (640, 64)
+    x = make_x(200, 1280, torch.bfloat16, seed=5).to(cuda)
+    y = q(x)
+    o = oracle.linear(bits(x), 0, q.weight_int8.cpu().numpy(), q.w_scale.cpu().numpy(), q.bias.cpu().numpy(), 0,
+                      bits(A.to(torch.bfloat16)), bits(B.to(torch.bfloat16)))
+    mx, mean = rel_errors(oracle.to_f32(bits(y), 0), o["y"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
 def test_int8linear_3d_and_views(cuda):
     """Leading dims are flattened and restored; a 3-D input gives the same result as its 2-D view
     (deploy/int8_exec.py:530-531); a row-slice input needs no copy."""
