@@ -498,7 +498,7 @@ class Int8Linear(nn.Module):
         x2 = x.reshape(-1, shape[-1])
         if x2.stride(1) != 1:
             x2 = x2.contiguous()
-        t = None
+        t = xq = sx = None
         fused = self.weight_packed is not None and self.lr_At is not None and x2.dtype == self.lr_A.dtype
         if fused:
             # quantizer and low-rank down-projection from one pass over x (deploy/int8_exec.py:390-391)
@@ -515,10 +515,9 @@ class Int8Linear(nn.Module):
                 t = t.to(x2.dtype)
         t_epi = None if t is None or self.lr_Bt is None else t[:, :self.lr_Bt.shape[1]]
         if t is not None and t_epi is None:
-            return self._forward_lr_after(x2, shape, xq if fused else None, sx if fused else None, t, row_idx, out,
-                                          out_row_idx)
+            return self._forward_lr_after(x2, shape, xq, sx, t, row_idx, out, out_row_idx)
         if self.weight_packed is not None:
-            if not fused:
+            if xq is None:
                 xq, sx = quant_rows_packed(x2, row_idx)
             y = int8_gemm_packed(xq, sx, self.weight_packed, self._scale_k(), self.bias, sx.shape[0],
                                  self.out_features, self.in_features, x2.dtype, t=t_epi, l2t=self._lr_bt(x2.dtype),
