@@ -91,6 +91,8 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert lib.pq_quant_rows(p16, 0, (1 << 26) + 64, 64, 64, nul, p16, p16, nul) == L.PQ_ESHAPE
     assert b"32-bit dispatch" in lib.pq_last_error()
     assert lib.pq_pack_k64(p16, 1 << 31, 64 * 1024, 64 * 1024, p16, nul) == L.PQ_ESHAPE
+    assert lib.pq_int8_gemm_i32(p16, 64, p16, 64, p16, 1 << 16, 1 << 30, 1 << 16, 64, nul) == L.PQ_ESHAPE
+    assert b"32-bit dispatch" in lib.pq_last_error()
     assert lib.pq_dequant_epilogue(nul, nul, nul, nul, nul, 128, 0, 8, 128, nul) == L.PQ_EINVAL
     # routing geometry and fusion
     assert lib.pq_route_union_rows(nul, 16, 16, 16, 2, 256, 256, p16, p16, nul) == L.PQ_EINVAL
