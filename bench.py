@@ -38,6 +38,15 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 3 device-to-device copies of BYTES (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE "
                          "against a plain copy kernel of known size) and exit")
+    ap.add_argument("--no-side", action="store_true",
+                    help="skip the side measurements (routing kernels, SDXL small-M launches, weight fold), e.g. for "
+                         "profiler runs that should hold the layer's kernels only")
+    ap.add_argument("--blaslt", action="store_true",
+                    help="only compare the int32-output GEMM with hipBLASLt's (torch._int_mm) on the config's "
+                         "operands, like for like, and print one JSON line")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only run the register-only MFMA throughput probe (random / constant / zero operands, int8 "
+                         "and fp16 MFMA) and print one JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the INT8 executor "
@@ -62,7 +71,13 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": src.numel() * 4}), flush=True)
         return 0
+    if args.mfma_ceiling:
+        print(json.dumps(mfma_ceiling(dev)), flush=True)
+        return 0
     cfg = CONFIGS[args.config]
+    if args.blaslt:
+        print(json.dumps(blaslt_compare(dev, cfg)), flush=True)
+        return 0
     lin = make_linear(cfg.K, cfg.N, cfg.lowrank, cfg.bias, dtype=cfg.dtype)
     q = E.Int8Linear(lin, device=dev, group_size=cfg.group)
     x = make_x(cfg.M, cfg.K, cfg.dtype).to(dev)
@@ -161,9 +176,10 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(cfg, lin, args.cpu_rows, args.cpu_iters)
-    routing = route_bench(dev, not args.no_cpu) if cfg.routed else None
-    launch = launch_bench(dev) if cfg.group else None
-    fold = fold_bench(dev, cfg) if cfg.name == "c1" else None
+    side = not args.no_side
+    routing = route_bench(dev, not args.no_cpu) if cfg.routed and side else None
+    launch = launch_bench(dev) if cfg.group and side else None
+    fold = fold_bench(dev, cfg) if cfg.name == "c1" and side else None
 
     res = {
         "metric": METRIC,
@@ -211,6 +227,111 @@ def main() -> int:
     }
     print(json.dumps(res), flush=True)
     return 0
+
+
+def blaslt_compare(dev, cfg):
+    """The same int8 operands through hipBLASLt (torch._int_mm: int32 [M, N] out, no epilogue) and through this build's
+    GEMM with int32 output (packed and row-major operands), and the fused bf16 layer GEMM for reference. Each: 2
+    warm-up calls, then 10 calls interleaved round-robin across the variants, each timed by its own HIP event pair on
+    the launch stream; medians reported."""
+    import torch
+
+    from pyraquant_amd import int8_exec as E
+
+    g = torch.Generator(device=dev).manual_seed(3)
+    xq = torch.randint(-127, 128, (cfg.M, cfg.K), generator=g, device=dev, dtype=torch.int8)
+    wq = torch.randint(-127, 128, (cfg.N, cfg.K), generator=g, device=dev, dtype=torch.int8)
+    sx = torch.rand(cfg.M, generator=g, device=dev) * 0.02 + 0.001
+    sw = torch.rand(cfg.N, generator=g, device=dev) * 0.001 + 1e-4
+    bias = torch.randn(cfg.N, generator=g, device=dev) * 0.01
+    xp, wp = E.pack_k64(xq), E.pack_k64(wq)
+    out = torch.empty(cfg.M, cfg.N, dtype=torch.bfloat16, device=dev)
+    wt = wq.t()
+    variants = {
+        "hipblaslt_int_mm_i32": lambda: torch._int_mm(xq, wt),
+        "pq_int8_gemm_packed_i32": lambda: E.int8_gemm_packed(xp, None, wp, None, None, cfg.M, cfg.N, cfg.K, torch.int32),
+        "pq_int8_gemm_i32_rowmajor": lambda: E.int8_gemm_i32(xq, wq),
+        "pq_int8_gemm_packed_bf16_fused": lambda: E.int8_gemm_packed(xp, sx, wp, sw, bias, cfg.M, cfg.N, cfg.K,
+                                                                     torch.bfloat16, out=out),
+    }
+    ref = torch._int_mm(xq, wt)
+    same = {k: bool(torch.equal(f(), ref)) for k, f in variants.items() if k.endswith("i32") or "i32_" in k}
+    times = {k: [] for k in variants}
+    for f in variants.values():
+        f()
+        f()
+    torch.cuda.synchronize()
+    for _ in range(10):
+        for k, f in variants.items():
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            f()
+            e1.record()
+            torch.cuda.synchronize()
+            times[k].append(e0.elapsed_time(e1) * 1e3)
+    ops = 2.0 * cfg.M * cfg.N * cfg.K
+    res = {}
+    for k, v in times.items():
+        us = sorted(v)[len(v) // 2]
+        res[k] = {"us": round(us, 1), "TOPS": round(ops / us / 1e6, 1), "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)}
+    return {"blaslt_compare": res, "int32_equal_to_int_mm": same, "config": cfg.name, "M": cfg.M, "K": cfg.K, "N": cfg.N}
+
+
+def mfma_ceiling(dev):
+    """Register-only MFMA loops (pyraquant_amd/csrc/probe/mfma_ceiling.hip) over the whole chip: the throughput the
+    matrix cores sustain with no memory traffic at all, for random, constant and zero operands, at 1, 2 and 4 waves
+    per SIMD. int8: v_mfma_i32_32x32x32_i8 against 5.0 POP/s; fp16: v_mfma_f32_32x32x16_f16 on the fp16 images of
+    int8 codes against 2.5 PFLOP/s; int8 again in 8-wave workgroups, with and without a static issue priority for
+    waves 0-3. Each case: one warm-up launch, then the median of 3 launches timed by HIP events
+    on the launch stream (about 20 ms each)."""
+    import ctypes
+
+    import torch
+
+    from pyraquant_amd import build as B
+
+    lib = ctypes.CDLL(B.PROBE_PATH)
+    lib.pq_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                  ctypes.c_void_p]
+    lib.pq_probe_mfma.restype = ctypes.c_int
+    g = torch.Generator().manual_seed(7)
+    codes = {"random": torch.randint(-127, 128, (16 * 64 * 16,), generator=g, dtype=torch.int32),
+             "constant": torch.full((16 * 64 * 16,), 90, dtype=torch.int32),
+             "zero": torch.zeros(16 * 64 * 16, dtype=torch.int32)}
+    stream = torch.cuda.current_stream(dev)
+    sink = torch.empty(256 * 4 * 256, dtype=torch.int32, device=dev)
+    cases = []
+    # (kind, MFMA, ops per instruction, peak, waves per workgroup, operand patterns, waves per SIMD)
+    plan = ((0, "i32_32x32x32_i8", 65536, INT8_PEAK_TOPS, 4, ("random", "constant", "zero"), (1, 2, 4)),
+            (1, "f32_32x32x16_f16", 32768, INT8_PEAK_TOPS / 2, 4, ("random", "constant", "zero"), (1, 2, 4)),
+            (2, "i32_32x32x32_i8 8-wave WG", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)),
+            (3, "i32_32x32x32_i8 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)))
+    for kind, name, per_inst, peak, wpb, patterns, wps_list in plan:
+        for pattern in patterns:
+            c = codes[pattern]
+            # int8: the bytes themselves; fp16: 8 codes per 16-byte fragment as fp16 values (exact)
+            src = (c[: 16 * 64 * 16].to(torch.int8) if kind != 1 else c[: 16 * 64 * 8].to(torch.float16)).to(dev)
+            for wps in wps_list:
+                blocks, iters = 256 * wps * 4 // wpb, 100000 // wps
+                call = lambda: lib.pq_probe_mfma(kind, ctypes.c_void_p(src.data_ptr()), blocks, iters,
+                                                 ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
+                assert call() == 0, "probe launch failed"
+                ms = []
+                for _ in range(3):
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(stream)
+                    call()
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    ms.append(e0.elapsed_time(e1))
+                t = sorted(ms)[1] * 1e-3
+                ops = float(blocks) * wpb * iters * 8 * per_inst
+                rate = ops / t / 1e12
+                cases.append({"mfma": name, "operands": pattern, "waves_per_simd": wps, "ms": round(t * 1e3, 3),
+                              "TOPS": round(rate, 1), "frac_of_peak": round(rate / peak, 4)})
+                print(f"[mfma-ceiling] {name} {pattern:8s} {wps} waves/SIMD: {rate:8.1f} TOP/s "
+                      f"({100 * rate / peak:5.1f} % of {peak:.0f})", flush=True)
+    return {"mfma_ceiling": cases, "gpu": torch.cuda.get_device_name(dev)}
 
 
 def fold_bench(dev, cfg):

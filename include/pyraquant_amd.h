@@ -163,6 +163,29 @@ int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, 
                         int64_t K, hipStream_t stream);
 
 /*
+ * Bytes of workspace pq_int8_linear needs for M rows, K inputs and R columns of t (R = 0: no low-rank branch):
+ * the packed codes, the row scales and t, each slice starting on a 256-byte boundary. -1 for a bad argument.
+ * No reference counterpart (the reference allocates the three tensors per call with torch.empty,
+ * deploy/int8_exec.py:225-226, 390).
+ */
+int64_t pq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t R);
+
+/*
+ * A whole Int8Linear layer in one call: y = Linear(x) as pq_quant_rows_lowrank (R > 0) or pq_quant_rows_packed
+ * (R == 0) followed by pq_int8_gemm_packed, with the codes, row scales and t staged in `workspace` (at least
+ * pq_int8_linear_workspace_size(M, K, R) bytes, 256-byte aligned; its contents on entry do not matter, and it is
+ * in use until the GEMM has run on `stream`). x [M, K] bf16/fp16 (row stride ldx); w_packed the packed K64
+ * weights [N, K]; s_w [N] (group 0) or [K/32, N] (group 32); bias [N] fp32 or NULL; l1t [R, K] and l2t [N, Re] in
+ * x's dtype (R a multiple of 32 up to 128, Re in {16, 32, 64} and Re <= R: the first Re columns of t enter the
+ * epilogue), or NULL with R = Re = 0; y [M, N] in x's dtype with row stride ldy. Same results as the two calls.
+ * Replaces the body of `Int8Linear.forward` (deploy/int8_exec.py:382-393): one C call per layer.
+ */
+int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
+                   const float* s_w, int64_t group, const float* bias, const void* l1t, int64_t R, const void* l2t,
+                   int64_t Re, void* y, int64_t ldy, int64_t N, void* workspace, int64_t ws_bytes,
+                   hipStream_t stream);
+
+/*
  * Repack a row-major int8 matrix src [R, K] (row stride lds, K % 64 == 0) into the packed K64 layout at dst
  * (ceil(R / 16) * 16 * K bytes, 16-byte aligned); padding rows are written as zeros. One-off at weight
  * conversion. No reference counterpart (the reference's Triton GEMM reads W_int8 row-major,

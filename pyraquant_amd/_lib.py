@@ -37,6 +37,8 @@ EXPORTS = (
     "pq_gather_rows",
     "pq_fuse_patches",
     "pq_fold_weight",
+    "pq_int8_linear_workspace_size",
+    "pq_int8_linear",
 )
 
 _p = ctypes.c_void_p
@@ -65,6 +67,9 @@ _SIGNATURES = {
     "pq_fuse_patches": ([_p, _i64, _p, _i64, _p, _p, _p, _i64, ctypes.c_float, _i64, _i64, _i64, _i32, _p, _i64, _p],
                         ctypes.c_int),
     "pq_fold_weight": ([_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p], ctypes.c_int),
+    "pq_int8_linear_workspace_size": ([_i64, _i64, _i64], _i64),
+    "pq_int8_linear": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p],
+                       ctypes.c_int),
 }
 
 _lib = None

@@ -1,0 +1,80 @@
+// One call per Int8Linear layer: the quantizer (with the low-rank down-projection when the layer has one) and the
+// fused GEMM, with the codes, row scales and t staged in a workspace between the two kernels
+// (reference: Int8Linear.forward, deploy/int8_exec.py:382-393).
+//
+// Workspace layout for M rows, K inputs and R columns of t (offsets rounded up to 256 bytes):
+//   [0, QB)           packed K64 codes, QB = ceil(M / 16) * 16 * K bytes
+//   [SO, SO + 4 M)    fp32 row scales, SO = round256(QB)
+//   [TO, TO + 2 M R)  16-bit t [M, R], TO = SO + round256(4 M)
+// The quantizer writes every byte the GEMM reads (padding code rows included), so the workspace needs no clearing
+// and may hold anything on entry.
+#include "pq_common.h"
+
+namespace pq {
+namespace {
+
+constexpr int64_t round256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+struct LayerSlices {
+  int64_t scales, t, total;
+};
+
+LayerSlices layer_slices(int64_t M, int64_t K, int64_t R) {
+  LayerSlices s;
+  s.scales = round256(((M + 15) / 16) * 16 * K);
+  s.t = s.scales + round256(4 * M);
+  s.total = s.t + 2 * M * R;
+  return s;
+}
+
+}  // namespace
+
+// The layer over a workspace the caller provides (shared by pq_int8_linear and its allocation-free variant).
+int run_layer(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
+              const float* s_w, int64_t group, const float* bias, const void* l1t, int64_t R, const void* l2t,
+              int64_t Re, void* y, int64_t ldy, int64_t N, uint8_t* ws, hipStream_t stream) {
+  const LayerSlices sl = layer_slices(M, K, R);
+  int8_t* const q = reinterpret_cast<int8_t*>(ws);
+  float* const s = reinterpret_cast<float*>(ws + sl.scales);
+  void* const t = R ? static_cast<void*>(ws + sl.t) : nullptr;
+  int st = R ? pq_quant_rows_lowrank(x, x_dtype, M, K, ldx, M, nullptr, l1t, R, q, s, t, R, stream)
+             : pq_quant_rows_packed(x, x_dtype, M, K, ldx, nullptr, q, s, stream);
+  if (st != PQ_OK) return st;
+  return pq_int8_gemm_packed(q, w_packed, s, s_w, group, bias, R ? t : nullptr, R, R ? l2t : nullptr, Re, x_dtype, y,
+                             ldy, x_dtype, nullptr, M, N, K, stream);
+}
+
+int check_layer(int64_t M, int64_t K, int64_t N, int64_t R, int64_t Re, const void* l1t, const void* l2t,
+                const char* who) {
+  if (M < 0 || K < 64 || N < 64) return set_error(PQ_ESHAPE, "%s: bad shape M=%lld K=%lld N=%lld", who, (long long)M, (long long)K, (long long)N);
+  if (K % 64 || N % 64) return set_error(PQ_ESHAPE, "%s: need K %% 64 == 0 and N %% 64 == 0", who);
+  if (R < 0 || Re < 0 || (R == 0) != (Re == 0) || (R && (!l1t || !l2t)))
+    return set_error(PQ_EINVAL, "%s: a low-rank branch needs l1t, l2t and both ranks (R=%lld, Re=%lld)", who,
+                     (long long)R, (long long)Re);
+  if (R && Re > R) return set_error(PQ_ESHAPE, "%s: epilogue rank %lld exceeds the %lld columns of t", who, (long long)Re, (long long)R);
+  return PQ_OK;
+}
+
+}  // namespace pq
+
+using namespace pq;
+
+extern "C" int64_t pq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t R) {
+  if (M < 0 || K < 1 || R < 0) return -1;
+  return layer_slices(M, K, R).total;
+}
+
+extern "C" int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+                              const int8_t* w_packed, const float* s_w, int64_t group, const float* bias,
+                              const void* l1t, int64_t R, const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N,
+                              void* workspace, int64_t ws_bytes, hipStream_t stream) {
+  int st = check_layer(M, K, N, R, Re, l1t, l2t, "pq_int8_linear");
+  if (st != PQ_OK || M == 0) return st;
+  const int64_t need = layer_slices(M, K, R).total;
+  if (!workspace || ws_bytes < need)
+    return set_error(PQ_ESHAPE, "pq_int8_linear: the workspace holds %lld bytes, the layer needs %lld", (long long)ws_bytes,
+                     (long long)need);
+  if ((uintptr_t)workspace % 256) return set_error(PQ_EALIGN, "pq_int8_linear: the workspace must be 256-byte aligned");
+  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, R, l2t, Re, y, ldy, N,
+                   static_cast<uint8_t*>(workspace), stream);
+}

@@ -429,6 +429,21 @@ class Int8Linear(nn.Module):
             self.lr_Bt = None
         del w
 
+    # Buffers the kernels read as fp32 whatever the model's dtype: a module-wide cast (.to(torch.bfloat16), .half())
+    # moves them with the module but leaves their dtype, so the kernels never see 16-bit scales or bias. (The
+    # reference's buffers follow the cast and its Triton kernels load any float type, deploy/int8_exec.py:356-362;
+    # keeping fp32 keeps its pre-cast precision.)
+    _FP32_BUFFERS = ("w_scale", "w_scale_gn", "bias")
+
+    def _apply(self, fn, recurse=True):
+        keep = {n: self._buffers[n] for n in self._FP32_BUFFERS if self._buffers.get(n) is not None}
+        super()._apply(fn, recurse)
+        for n, old in keep.items():
+            new = self._buffers[n]
+            if new is not None and new.dtype != torch.float32:
+                self._buffers[n] = old.to(new.device)
+        return self
+
     def _scale_k(self) -> torch.Tensor:
         return self.w_scale_gn if self.group_size else self.w_scale
 
@@ -441,10 +456,10 @@ class Int8Linear(nn.Module):
         return self.lr_Bt
 
     def _forward_direct(self, x: torch.Tensor) -> Optional[torch.Tensor]:
-        """The common layer call (no routing arguments, packed weights) with the host work cut to the two C calls:
-        codes, scales and t share one workspace allocation, operands go as raw pointers, the stream is the raw
-        current stream. Same kernels and arguments as the general path, so the same bits; returns None when a
-        precondition of this path does not hold."""
+        """The common layer call (no routing arguments, packed weights) with the host work cut to one C call,
+        pq_int8_linear: codes, scales and t share one workspace allocation, operands go as raw pointers, the stream
+        is the raw current stream. Same kernels and arguments as the general path, so the same bits; returns None
+        when a precondition of this path does not hold."""
         dt = x.dtype
         code = _DIRECT_DTYPES.get(dt)
         K, N = self.in_features, self.out_features
@@ -459,31 +474,23 @@ class Int8Linear(nn.Module):
         Re = 0 if self.lr_Bt is None else self.lr_Bt.shape[1]         # rank of the epilogue
         if R and (self.lr_At.dtype != dt or self.lr_Bt.dtype != dt):
             return None
+        # the GEMM reads these as fp32 through raw pointers: anything else goes to the general path, which asserts
+        sk = self._scale_k()
+        if sk.dtype != torch.float32 or sk.device != x.device or not sk.is_contiguous():
+            return None
+        if self.bias is not None and (self.bias.dtype != torch.float32 or self.bias.device != x.device):
+            return None
         M = x2.shape[0]
         dev = x2.device
-        q_bytes = packed_rows(M) * K
-        s_off = (q_bytes + 255) & ~255
-        t_off = s_off + ((4 * M + 255) & ~255)
-        ws = torch.empty(t_off + 2 * M * R, dtype=torch.uint8, device=dev)
-        out = torch.empty((M, N), dtype=dt, device=dev)
-        base = ws.data_ptr()
-        stream = _raw_stream(dev)
         L = _lib.load()
-        if R:
-            st = L.pq_quant_rows_lowrank(x2.data_ptr(), code, M, K, x2.stride(0), M, None, self.lr_At.data_ptr(), R,
-                                         base, base + s_off, base + t_off, R, stream)
-            what = "quant_rows_lowrank"
-        else:
-            st = L.pq_quant_rows_packed(x2.data_ptr(), code, M, K, x2.stride(0), None, base, base + s_off, stream)
-            what = "quant_rows_packed"
+        ws = torch.empty(L.pq_int8_linear_workspace_size(M, K, R), dtype=torch.uint8, device=dev)
+        out = torch.empty((M, N), dtype=dt, device=dev)
+        st = L.pq_int8_linear(x2.data_ptr(), code, M, K, x2.stride(0), self.weight_packed.data_ptr(), sk.data_ptr(),
+                              self.group_size, None if self.bias is None else self.bias.data_ptr(),
+                              self.lr_At.data_ptr() if R else None, R, self.lr_Bt.data_ptr() if R else None, Re,
+                              out.data_ptr(), N, N, ws.data_ptr(), ws.numel(), _raw_stream(dev))
         if st:
-            _lib.check(st, what)
-        st = L.pq_int8_gemm_packed(base, self.weight_packed.data_ptr(), base + s_off, self._scale_k().data_ptr(),
-                                   self.group_size, None if self.bias is None else self.bias.data_ptr(),
-                                   base + t_off if R else None, R, self.lr_Bt.data_ptr() if R else None, Re,
-                                   code, out.data_ptr(), N, code, None, M, N, K, stream)
-        if st:
-            _lib.check(st, "int8_gemm_packed")
+            _lib.check(st, "int8_linear")
         return out.reshape(*x.shape[:-1], N)
 
     def forward(self, x: torch.Tensor, row_idx: Optional[torch.Tensor] = None,

@@ -44,12 +44,14 @@ CONFIGS = {
 
 
 def make_x(M: int, K: int, dtype=torch.bfloat16, seed: int = 42, outlier_frac: float = 0.005,
-           outlier_scale: float = 20.0) -> torch.Tensor:
-    g = torch.Generator().manual_seed(seed)
-    x = torch.randn(M, K, generator=g)
+           outlier_scale: float = 20.0, device: Optional[torch.device] = None) -> torch.Tensor:
+    """Activations of the configs. With `device`, the same distribution is drawn by that device's generator (fast
+    at full sizes; a different random stream from the CPU one)."""
+    g = torch.Generator(device=device if device is not None else "cpu").manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=device)
     n_out = int(round(outlier_frac * K))
     if n_out:
-        cols = torch.randperm(K, generator=g)[:n_out]
+        cols = torch.randperm(K, generator=g, device=device)[:n_out]
         x[:, cols] *= outlier_scale
     return x.to(dtype)
 

@@ -1,0 +1,109 @@
+"""Full-size parity: Int8Linear.forward at every BASELINE configuration's real shape, checked against the CPU oracle
+on sampled rows (deploy/int8_exec.py:382-393 for the layer, :303-309 for the epilogue order).
+
+Each case runs the whole layer on the GPU (the module's own path: the fused quantizer + low-rank pass or the packed
+quantizer, then the packed GEMM with its epilogue), then takes 64 seeded random rows plus the last 40 rows (the last,
+possibly ragged, tiles) and computes those rows on the CPU with the oracle from the module's own int8 weights:
+* int8 codes and row scales bit-exact (the codes are read back from the packed buffer the layer's first kernel
+  wrote, through the same entry point the module calls);
+* without a low-rank branch (c3), the 16-bit outputs bit-exact;
+* with one, the normwise bar (max 1e-2, mean 5e-3) and the element-wise bar of conftest.elem_violation.
+The routed case (c4) runs on the full 65536-row canvas: the routed rows land where the gather list says, every other
+row of the canvas is left as it was.
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import MAX_REL, MEAN_REL, bits, dcode, elem_violation, rel_errors
+
+pytestmark = pytest.mark.gpu
+
+
+def _sample_rows(M: int, seed: int) -> torch.Tensor:
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.cat([torch.randperm(M - 40, generator=g)[:64], torch.arange(M - 40, M)])
+    return rows.sort().values
+
+
+def _packed_rows(qp: torch.Tensor, rows: torch.Tensor, K: int) -> np.ndarray:
+    """Rows of a packed K64 code buffer, back in row-major order (the layout's definition: block (rb, kt) at
+    (rb * KT + kt) * 1024, row r' = r % 16 at 64 r', 16-byte chunk c at slot c ^ swz(r'))."""
+    from oracle import oracle as O
+
+    KT = K // 64
+    blocks = qp.view(-1, KT, 16, 4, 16)[(rows // 16).to(qp.device)].cpu().numpy()   # [n, KT, 16, 4, 16]
+    rr = (rows % 16).numpy()
+    n = rows.numel()
+    sel = blocks[np.arange(n), :, rr]                                                 # [n, KT, 4, 16]
+    slot = np.arange(4)[None, :] ^ O.k64_swz(rr)[:, None]                             # chunk c sits at slot[c]
+    out = np.take_along_axis(sel, slot[:, None, :, None], axis=2)
+    return out.reshape(n, K)
+
+
+def _first_stage(E, q, x2, row_idx=None):
+    """The codes, scales (and t) of the layer's first kernel, through the entry point Int8Linear.forward uses."""
+    if q.lr_At is not None:
+        return E.quant_rows_lowrank(x2, q.lr_At, row_idx)
+    xq, sx = E.quant_rows_packed(x2, row_idx)
+    return xq, sx, None
+
+
+def _check_rows(oracle, q, x_rows_bits, dt, y_rows, codes, scales):
+    """Oracle of the sampled rows from the module's own buffers; codes / scales exact, outputs to the bar."""
+    lr = q.lr_A is not None
+    o = oracle.linear(x_rows_bits, dt, q.weight_int8.cpu().numpy(), q.w_scale.cpu().numpy(),
+                      None if q.bias is None else q.bias.cpu().numpy(), q.group_size,
+                      bits(q.lr_A) if lr else None, bits(q.lr_B) if lr else None)
+    assert np.array_equal(codes, o["q"]), "int8 codes differ from the oracle"
+    assert np.array_equal(scales.view(np.uint32), o["s"].view(np.uint32)), "row scales differ from the oracle"
+    got = bits(y_rows)
+    if not lr:
+        assert np.array_equal(got, o["out"]), "outputs without a low-rank branch must be bit-exact"
+        return
+    y = oracle.to_f32(got, dt)
+    mx, mean = rel_errors(y, o["y"])
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    v = elem_violation(y, o["y"], oracle.to_f32(o["t"], dt), oracle.to_f32(bits(q.lr_B), dt))
+    assert v <= 1.0, v
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2a", "c2b", "c3_1280", "c3_5120"])
+def test_layer_full_size(oracle, cuda, cfg):
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import CONFIGS, make_linear, make_x
+
+    c = CONFIGS[cfg]
+    print(f"[fullsize] {cfg} M={c.M} K={c.K} N={c.N} rank={c.lowrank} group={c.group}", flush=True)
+    q = E.Int8Linear(make_linear(c.K, c.N, c.lowrank, c.bias, dtype=c.dtype), device=cuda, group_size=c.group)
+    x = make_x(c.M, c.K, c.dtype, seed=7, device=cuda)
+    y = q(x)
+    assert y.shape == (c.M, c.N) and y.dtype == c.dtype
+    xq, sx, _ = _first_stage(E, q, x)
+    rows = _sample_rows(c.M, seed=c.M + c.N)
+    rd = rows.to(cuda)
+    _check_rows(oracle, q, bits(x[rd]), dcode(c.dtype), y[rd], _packed_rows(xq, rows, c.K), sx[rd].cpu().numpy())
+
+
+def test_routed_full_canvas(oracle, cuda):
+    """c4: config 4's 33,316 routed rows gathered from the 65536-token x and scattered into the 65536-row canvas."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import CONFIGS, make_linear, make_x, routed_rows
+
+    c = CONFIGS["c4"]
+    q = E.Int8Linear(make_linear(c.K, c.N, c.lowrank, c.bias), device=cuda)
+    x = make_x(c.M, c.K, seed=8, device=cuda)
+    ri = routed_rows(cuda)
+    M = ri.numel()
+    print(f"[fullsize] c4 routed M={M} of {c.M}", flush=True)
+    canvas = make_x(c.M, c.N, seed=9, outlier_frac=0.0, device=cuda)
+    before = canvas.clone()
+    q(x, row_idx=ri, out=canvas, out_row_idx=ri)
+    xq, sx, _ = _first_stage(E, q, x, ri)
+    m = _sample_rows(M, seed=4)                      # positions in the routed list (the last 40: the ragged tile)
+    src = ri.cpu()[m].long()
+    _check_rows(oracle, q, bits(x[src.to(cuda)]), dcode(c.dtype), canvas[src.to(cuda)], _packed_rows(xq, m, c.K),
+                sx[m.to(cuda)].cpu().numpy())
+    keep = torch.ones(c.M, dtype=torch.bool, device=cuda)
+    keep[ri.long()] = False
+    assert torch.equal(canvas[keep], before[keep]), "rows outside the gather list must keep the cached canvas"

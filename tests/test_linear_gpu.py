@@ -406,3 +406,37 @@ def test_module_conversion_and_warmup(cuda):
     q = u.down.to_q
     assert torch.equal(sdxl.fast_gemm_fused(xq, sx, q.weight_int8, q.w_scale, q.bias, torch.float16),
                        E.int8_gemm_fused(xq, sx, q.weight_int8, q.w_scale, q.bias, torch.float16))
+
+
+def test_int8linear_module_cast(oracle, cuda):
+    """A module-wide cast (.to(torch.bfloat16), .half()) keeps the fp32 scale and bias buffers fp32, so the kernels,
+    which read them through raw pointers, never see 16-bit scales: the bf16 outputs are unchanged bit for bit, and an
+    fp16 call after .half() equals a module built in fp16 from the same weights (codes / scales exact against the
+    oracle, outputs within tolerance)."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    for group in (0, 32):
+        lin = make_linear(1280, 640, 0 if group else 32, True)
+        q = E.Int8Linear(lin, device=cuda, group_size=group)
+        x = make_x(200, 1280, seed=group + 1).to(cuda)
+        y = q(x)
+        q.to(torch.bfloat16)
+        for name in ("w_scale", "bias") + (("w_scale_gn",) if group else ()):
+            assert getattr(q, name).dtype == torch.float32, name
+        assert torch.equal(q(x), y)
+        q.half()
+        assert q.w_scale.dtype == torch.float32 and q.bias.dtype == torch.float32
+        xh = x.half()
+        yh = q(xh)
+        E.DIRECT_CALLS = False
+        try:
+            assert torch.equal(q(xh), yh)          # the general path gives the same bits
+        finally:
+            E.DIRECT_CALLS = True
+        o = _oracle_module(oracle, q, xh)
+        if group:
+            assert np.array_equal(bits(yh), o["out"])
+        else:
+            mx, mean = rel_errors(oracle.to_f32(bits(yh), 1), o["y"])
+            assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
