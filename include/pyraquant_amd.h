@@ -186,6 +186,24 @@ int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t
                    hipStream_t stream);
 
 /*
+ * pq_int8_linear without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference, which
+ * allocates its intermediates with torch per call (deploy/int8_exec.py:225-226, 390). The staging lives in a device
+ * array of the library, pq_int8_linear_noalloc_max_bytes() bytes (64 MiB) on each GPU it runs on, held until the
+ * process ends; a layer whose pq_int8_linear_workspace_size(M, K, R) exceeds that is refused with PQ_ESHAPE before
+ * any work (FLUX's 1K-stage and SDXL's layers fit; FLUX's 4K stage does not). Nothing is allocated, freed or
+ * cleared per call. `stream` must belong to the current device. Every call on a GPU uses that GPU's one array:
+ * calls that overlap on one GPU (other streams, other threads) race, so serialise them. Arguments and results as
+ * pq_int8_linear.
+ */
+int pq_int8_linear_noalloc(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
+                           const float* s_w, int64_t group, const float* bias, const void* l1t, int64_t R,
+                           const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N, hipStream_t stream);
+
+/* Bytes of the device array behind pq_int8_linear_noalloc (its largest staging). No reference counterpart. */
+int64_t pq_int8_linear_noalloc_max_bytes(void);
+
+/*
  * Repack a row-major int8 matrix src [R, K] (row stride lds, K % 64 == 0) into the packed K64 layout at dst
  * (ceil(R / 16) * 16 * K bytes, 16-byte aligned); padding rows are written as zeros. One-off at weight
  * conversion. No reference counterpart (the reference's Triton GEMM reads W_int8 row-major,

@@ -39,6 +39,8 @@ EXPORTS = (
     "pq_fold_weight",
     "pq_int8_linear_workspace_size",
     "pq_int8_linear",
+    "pq_int8_linear_noalloc",
+    "pq_int8_linear_noalloc_max_bytes",
 )
 
 _p = ctypes.c_void_p
@@ -70,6 +72,9 @@ _SIGNATURES = {
     "pq_int8_linear_workspace_size": ([_i64, _i64, _i64], _i64),
     "pq_int8_linear": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p],
                        ctypes.c_int),
+    "pq_int8_linear_noalloc": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p],
+                               ctypes.c_int),
+    "pq_int8_linear_noalloc_max_bytes": ([], _i64),
 }
 
 _lib = None

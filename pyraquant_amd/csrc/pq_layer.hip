@@ -10,6 +10,8 @@
 // and may hold anything on entry.
 #include "pq_common.h"
 
+#include <mutex>
+
 namespace pq {
 namespace {
 
@@ -77,4 +79,66 @@ extern "C" int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t
   if ((uintptr_t)workspace % 256) return set_error(PQ_EALIGN, "pq_int8_linear: the workspace must be 256-byte aligned");
   return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, R, l2t, Re, y, ldy, N,
                    static_cast<uint8_t*>(workspace), stream);
+}
+
+// ---- allocation-free variant -------------------------------------------------------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph capture, serving loops, harnesses that forbid
+// hipMalloc): the workspace is this file-scope device array, one copy per GPU, held until the process ends. In host
+// code `scratch` names a host-side stand-in, not the device array: its device address comes from
+// hipGetSymbolAddress, once per device (with that device current), and only that address is passed to kernels.
+// Every call on a GPU shares that GPU's array, so calls that overlap on one GPU (two streams, two threads) race.
+// Nothing here needs clearing: the quantizer writes every byte of the slices the GEMM reads.
+constexpr int64_t kScratchBytes = 64LL << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};   // device address of `scratch` on each device, once looked up
+
+// Device address of this device's scratch array; the stream must belong to the current device.
+int device_scratch(hipStream_t stream, uint8_t** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(PQ_ELAUNCH, "pq_int8_linear_noalloc: no usable current device");
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess)
+      return set_error(PQ_EINVAL, "pq_int8_linear_noalloc: cannot query the stream's device");
+    if (sdev != dev)
+      return set_error(PQ_EINVAL, "pq_int8_linear_noalloc: the stream belongs to device %d, device %d is current",
+                       (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(PQ_ELAUNCH, "pq_int8_linear_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return PQ_OK;
+}
+}  // namespace
+
+extern "C" int64_t pq_int8_linear_noalloc_max_bytes(void) { return kScratchBytes; }
+
+extern "C" int pq_int8_linear_noalloc(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+                                      const int8_t* w_packed, const float* s_w, int64_t group, const float* bias,
+                                      const void* l1t, int64_t R, const void* l2t, int64_t Re, void* y, int64_t ldy,
+                                      int64_t N, hipStream_t stream) {
+  int st = check_layer(M, K, N, R, Re, l1t, l2t, "pq_int8_linear_noalloc");
+  if (st != PQ_OK || M == 0) return st;
+  const int64_t need = layer_slices(M, K, R).total;
+  if (need > kScratchBytes)
+    return set_error(PQ_ESHAPE,
+                     "pq_int8_linear_noalloc: M=%lld, K=%lld, R=%lld needs %lld bytes of staging, more than the %lld "
+                     "bytes of its device scratch; use pq_int8_linear with a workspace",
+                     (long long)M, (long long)K, (long long)R, (long long)need, (long long)kScratchBytes);
+  uint8_t* ws = nullptr;
+  st = device_scratch(stream, &ws);
+  if (st != PQ_OK) return st;
+  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, R, l2t, Re, y, ldy, N, ws, stream);
 }
