@@ -6,7 +6,8 @@
  * pointers, element strides and a HIP stream; nothing here allocates or frees device memory, and no
  * entry point synchronises the stream. All calls are asynchronous on `stream` (pass the caller's
  * current stream; torch: torch.cuda.current_stream().cuda_stream). The C API keeps no mutable global
- * state apart from the thread-local error text, so it may be called from several host threads.
+ * state apart from the thread-local error text and pq_int8_linear_noalloc's device array (one per GPU,
+ * see there), so every other entry point may be called from several host threads.
  *
  * Return value of every int-returning entry point: PQ_OK (0) or a negative PQ_E* code; the text of the
  * last error on the calling thread is available from pq_last_error().
@@ -55,6 +56,10 @@ extern "C" {
 #define PQ_BF16 0
 #define PQ_F16 1
 #define PQ_I32 2
+
+/* flag OR'ed into pq_int8_gemm_packed's out_dtype: accumulate into c instead of overwriting it,
+ * c[o, n] = round(c[o, n] + round(y)) (two 16-bit roundings, as torch adds two 16-bit tensors) */
+#define PQ_ACCUMULATE 0x100
 
 /* Version of this ABI (PQ_ABI_VERSION). No reference counterpart. */
 int pq_abi_version(void);
@@ -152,7 +157,10 @@ int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, int64_t K, 
  * Fused INT8 GEMM over packed K64 operands (ap: activation codes [M, K], wp: weights [N, K], both in the packed
  * K64 layout). Same math, epilogue, scatter and requirements as pq_int8_gemm (group 0: s_w [N]; group 32:
  * s_w [K/32, N] group-major); with out_dtype == PQ_I32, c receives the raw int32 accumulator (s_row, s_w, group,
- * bias, t, l2t, out_row_idx ignored; c 16-byte aligned, ldc % 4 == 0). This is the layer path of Int8Linear: the quantizer writes ap directly
+ * bias, t, l2t, out_row_idx ignored; c 16-byte aligned, ldc % 4 == 0). With out_dtype | PQ_ACCUMULATE (16-bit
+ * output, group 0), each output element is added to what c holds: c = round(c + round(y)), so a Linear split along
+ * its input accumulates its second half into the first half's output in the same pass that writes it
+ * (`SplitInLinear.forward`'s `L0(x0) + L1(x1)`, pyraquant/external_quant.py:191-192). This is the layer path of Int8Linear: the quantizer writes ap directly
  * (pq_quant_rows_packed) and the weights are packed once at conversion (pq_pack_k64).
  * Replaces `int8_gemm_fused` / `int8_gemm_lr` (deploy/int8_exec.py:202-212, 327-336) as called from
  * `Int8Linear.forward` (deploy/int8_exec.py:382-393).

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpqint8.s
 
 PQ_OK, PQ_EINVAL, PQ_ESHAPE, PQ_EALIGN, PQ_EDTYPE, PQ_ELAUNCH = 0, -1, -2, -3, -4, -5
 PQ_BF16, PQ_F16, PQ_I32 = 0, 1, 2
+PQ_ACCUMULATE = 0x100   # OR'ed into pq_int8_gemm_packed's out_dtype
 ABI_VERSION = 1
 
 # every entry point declared in include/pyraquant_amd.h

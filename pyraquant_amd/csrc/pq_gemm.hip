@@ -76,6 +76,17 @@ __device__ __forceinline__ void tile_coords(int bid, int nblocks, int tiles_m, i
   tn = r / gsize;
 }
 
+// c + y for 8 16-bit values (16 bytes): each sum in fp32, rounded to the 16-bit type (to nearest even), as torch adds
+// two 16-bit tensors. The accumulate mode's last step: the addend already holds a rounded output, y the new one.
+template <int DT>
+__device__ __forceinline__ v4u add_16x8(v4u c, v4u y) {
+  v4u r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    r[q] = pack2<DT>(lo16_to_f32<DT>(c[q]) + lo16_to_f32<DT>(y[q]), hi16_to_f32<DT>(c[q]) + hi16_to_f32<DT>(y[q]));
+  return r;
+}
+
 template <int LRDT>
 __device__ __forceinline__ v16f lr_mfma(v4i a, v4i b, v16f c) {
   if constexpr (LRDT == PQ_BF16) {
@@ -96,7 +107,7 @@ __device__ __forceinline__ v16f lr_mfma(v4i a, v4i b, v16f c) {
 // NTS: output stores carry the non-temporal hint (streamed past the L2). The large blocks' outputs (c1: 1.6 GB per
 // launch) are never re-read by the kernel, and keeping them out of the L2 leaves it to the operand tiles (measured
 // 0.5-1.3 % faster at c1 / c2b in the layer step).
-template <int TI, int TJ, int MODE, int LRS, int LRDT, int ODT, int CB = 2, bool NTS = false>
+template <int TI, int TJ, int MODE, int LRS, int LRDT, int ODT, int CB = 2, bool NTS = false, bool ACC = false>
 struct Epilogue {
   // CB = 2: the column operands of weight tile i + 1 load while tile i is computed (one workgroup per CU);
   // CB = 1: loaded right before use (two workgroups per CU hide the latency and the register budget is halved).
@@ -190,6 +201,26 @@ struct Epilogue {
     for (int j = 0; j < TJ; ++j) {
 #pragma unroll
       for (int ih = 0; ih < TI / 2; ++ih) {
+        // staging -> global: 8 lanes x 16 bytes per 128-byte row piece, 8 rows per store instruction
+        // row addresses: one 32 x 32 -> 64-bit product per scattered row (ldc < 2^31), or the lane's first row plus a
+        // wave-uniform offset
+        const int lr_ = lane >> 3, lc = lane & 7;
+        const int n = nbase + ih * 64 + lc * 8;
+        const bool nvalid = n < p.N;
+        const int ldc = (int)p.ldc;
+        uint16_t* const cn = static_cast<uint16_t*>(p.c) + n;
+        uint16_t* const cm = cn + (int64_t)(mbase + lr_) * ldc;
+        auto valid = [&](int s0) { return nvalid && mbase + j * 32 + s0 + lr_ < p.M; };
+        auto dst_of = [&](int s0) {
+          return p.out_row_idx ? cn + (int64_t)orows[mloc + j * 32 + s0 + lr_] * ldc : cm + (int64_t)(j * 32 + s0) * ldc;
+        };
+        v4u prev[4];
+        if constexpr (ACC) {
+          // accumulate into c: its current contents are fetched before the tiles are computed, hiding the latency
+#pragma unroll
+          for (int s0 = 0; s0 < 32; s0 += 8)
+            prev[s0 >> 3] = valid(s0) ? *reinterpret_cast<const v4u*>(dst_of(s0)) : v4u{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
         for (int ii = 0; ii < 2; ++ii) {
           const int i = 2 * ih + ii;
@@ -211,23 +242,12 @@ struct Epilogue {
           }
           tile(acc[i][j], j, 0, has_bias, stage + (lane & 31) * kPitchL + (ii * 32 + 4 * khalf) * 2);
         }
-        // staging -> global: 8 lanes x 16 bytes per 128-byte row piece, 8 rows per store instruction
-        // row addresses: one 32 x 32 -> 64-bit product per scattered row (ldc < 2^31), or the lane's first row plus a
-        // wave-uniform offset
-        const int lr_ = lane >> 3, lc = lane & 7;
-        const int n = nbase + ih * 64 + lc * 8;
-        const bool nvalid = n < p.N;
-        const int ldc = (int)p.ldc;
-        uint16_t* const cn = static_cast<uint16_t*>(p.c) + n;
-        uint16_t* const cm = cn + (int64_t)(mbase + lr_) * ldc;
 #pragma unroll
         for (int s0 = 0; s0 < 32; s0 += 8) {
-          const int row = s0 + lr_;
-          const int m = mbase + j * 32 + row;
-          const v4u v = *reinterpret_cast<const v4u*>(stage + row * kPitchL + lc * 16);
-          if (nvalid && m < p.M) {
-            uint16_t* const dst = p.out_row_idx ? cn + (int64_t)orows[mloc + j * 32 + row] * ldc
-                                                : cm + (int64_t)(j * 32 + s0) * ldc;
+          v4u v = *reinterpret_cast<const v4u*>(stage + (s0 + lr_) * kPitchL + lc * 16);
+          if (valid(s0)) {
+            uint16_t* const dst = dst_of(s0);
+            if constexpr (ACC) v = add_16x8<ODT>(prev[s0 >> 3], v);
             if constexpr (NTS) {
               __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(dst));
             } else {
@@ -343,9 +363,10 @@ struct Epilogue {
       for (int s0 = 0; s0 < 32 * TJ; s0 += RPI) {
         const int row = s0 + lr_;
         const int m = mbase + row;
-        const v4u v = *reinterpret_cast<const v4u*>(stage + row * kPitch + lc * 16);
+        v4u v = *reinterpret_cast<const v4u*>(stage + row * kPitch + lc * 16);
         if (nvalid && m < p.M) {
           uint16_t* const dst = p.out_row_idx ? cn + (int64_t)srow[row] * ldc : cm + (int64_t)s0 * ldc;
+          if constexpr (ACC) v = add_16x8<ODT>(*reinterpret_cast<const v4u*>(dst), v);   // accumulate into c
           if constexpr (NTS) {
             __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(dst));
           } else {
@@ -382,7 +403,7 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // WMW waves along m (2 or 4) times 2 along n; OCC workgroups per CU.
-template <int TI, int TJ, int WMW, int NS, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
+template <int TI, int TJ, int WMW, int NS, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT, bool ACC = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(128 * WMW, 128 * WMW),
                           amdgpu_waves_per_eu(OCC * WMW / 2, OCC * WMW / 2)))
 void gemm_dma_kernel(const GemmArgs p) {
@@ -402,7 +423,7 @@ void gemm_dma_kernel(const GemmArgs p) {
   constexpr int DPW = DW + DA + DS;
   // Epilogue operands through the ring (run_lds): the row and column slots must fit one stage each and the
   // operand DMA slots of one stage, and the output staging the remaining NS - 2 buffers.
-  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT, OCC * WMW == 2 ? 2 : 1, OCC == 1>;
+  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT, OCC * WMW == 2 ? 2 : 1, OCC == 1, ACC>;
   constexpr int kLrBytes = LRS * 16 * 2;                       // one low-rank row
   constexpr int kRowSlots = 2 + BM * kLrBytes / 1024, kColSlots = 2 + BN * kLrBytes / 1024;
   constexpr bool ELDS = MODE != kModeI32 && TI % 2 == 0 && NS >= 3 && BN <= 256 && BM <= 256 &&
@@ -707,13 +728,13 @@ constexpr int ring_stages() {
   return ns < 8 ? ns : 8;
 }
 
-template <int TI, int TJ, int WMW, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT>
+template <int TI, int TJ, int WMW, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT, bool ACC = false>
 int launch_dma(GemmArgs& a, hipStream_t stream) {
   constexpr int NS = ring_stages<TI, TJ, WMW, OCC, MODE>();
   dim3 grid;
   const int st = grid_of(a, 32 * TJ * WMW, 64 * TI, 128 * WMW, grid);
   if (st != PQ_OK) return st;
-  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, WMW, NS, OCC, PACKED, MODE, LRS, LRDT, ODT>), grid, dim3(128 * WMW), 0,
+  hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, WMW, NS, OCC, PACKED, MODE, LRS, LRDT, ODT, ACC>), grid, dim3(128 * WMW), 0,
                      stream, a);
   return check_launch("int8_gemm");
 }
@@ -730,42 +751,42 @@ inline bool big_tiles(const GemmArgs& a) {
 // 128 x 128 blocks of the problem (the small-problem tile).
 inline int64_t small_blocks(const GemmArgs& a) { return (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128); }
 
-template <bool PACKED, int MODE, int LRS, int LRDT, int ODT>
+template <bool PACKED, int MODE, int LRS, int LRDT, int ODT, bool ACC>
 int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
   if constexpr (MODE == kModeGroup32) {
     // fp32 accumulators live in VGPRs (the VALU rescales them every group): 128 x 128 blocks, two per CU; with
     // fewer than 512 of them, 128 x 64 blocks (the VALU-bound kernel then spreads over twice the CUs: measured
     // 1.2-1.5x faster at M = 2048 for the SDXL shapes, slower once the 128 x 128 blocks fill the chip)
-    if (small_blocks(a) < 512) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
-    return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    if (small_blocks(a) < 512) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
+    return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
   } else {
-    if (big_tiles(a)) return launch_dma<4, 2, 4, 1, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    if (big_tiles(a)) return launch_dma<4, 2, 4, 1, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
     // fewer 128 x 128 blocks than half the CUs: 128 x 64 blocks (measured 1.3x faster at 80 blocks, even at 160)
-    if (small_blocks(a) < 128) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
-    return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT>(a, stream);
+    if (small_blocks(a) < 128) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
+    return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
   }
 }
 
 // low-rank slices held in registers: exactly R / 16 (R = 16, 32 or 64)
-template <bool PACKED, int MODE, int DT>
+template <bool PACKED, int MODE, int DT, bool ACC>
 int dispatch_rank(GemmArgs& a, hipStream_t stream) {
-  if (a.R == 32) return dispatch_tiles<PACKED, MODE, 2, DT, DT>(a, stream);
-  if (a.R == 16) return dispatch_tiles<PACKED, MODE, 1, DT, DT>(a, stream);
-  return dispatch_tiles<PACKED, MODE, 4, DT, DT>(a, stream);
+  if (a.R == 32) return dispatch_tiles<PACKED, MODE, 2, DT, DT, ACC>(a, stream);
+  if (a.R == 16) return dispatch_tiles<PACKED, MODE, 1, DT, DT, ACC>(a, stream);
+  return dispatch_tiles<PACKED, MODE, 4, DT, DT, ACC>(a, stream);
 }
 
 // The low-rank operands t / l2t share the output's 16-bit type (the reference computes t in lr_A's dtype and
 // Int8Linear keeps lr_A in the model dtype, deploy/int8_exec.py:371-390).
-template <bool PACKED, int MODE>
+template <bool PACKED, int MODE, bool ACC = false>
 int dispatch_dtypes(GemmArgs& a, bool has_lr, int lr_dtype, int out_dtype, hipStream_t stream) {
   if (has_lr && lr_dtype != out_dtype)
     return set_error(PQ_EDTYPE, "pq_int8_gemm: low-rank dtype %d must equal the output dtype %d", lr_dtype, out_dtype);
   if (out_dtype == PQ_BF16) {
-    if (!has_lr) return dispatch_tiles<PACKED, MODE, 0, PQ_BF16, PQ_BF16>(a, stream);
-    return dispatch_rank<PACKED, MODE, PQ_BF16>(a, stream);
+    if (!has_lr) return dispatch_tiles<PACKED, MODE, 0, PQ_BF16, PQ_BF16, ACC>(a, stream);
+    return dispatch_rank<PACKED, MODE, PQ_BF16, ACC>(a, stream);
   } else if (out_dtype == PQ_F16) {
-    if (!has_lr) return dispatch_tiles<PACKED, MODE, 0, PQ_F16, PQ_F16>(a, stream);
-    return dispatch_rank<PACKED, MODE, PQ_F16>(a, stream);
+    if (!has_lr) return dispatch_tiles<PACKED, MODE, 0, PQ_F16, PQ_F16, ACC>(a, stream);
+    return dispatch_rank<PACKED, MODE, PQ_F16, ACC>(a, stream);
   }
   return set_error(PQ_EDTYPE, "pq_int8_gemm: unsupported output dtype %d", out_dtype);
 }
@@ -851,6 +872,8 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
                                    int64_t group, const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R,
                                    int32_t lr_dtype, void* c, int64_t ldc, int32_t out_dtype,
                                    const int32_t* out_row_idx, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+  const bool accumulate = (out_dtype & PQ_ACCUMULATE) != 0;
+  out_dtype &= ~PQ_ACCUMULATE;
   if (M < 0 || N < 1 || K < 1) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: bad shape");
   if (K % 64 != 0 || N % 64 != 0)
     return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: need K %% 64 == 0 and N %% 64 == 0 (K=%lld, N=%lld)",
@@ -864,6 +887,8 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
   GemmArgs args{};
   args.a = ap; args.w = wp; args.c = c;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
+  if (accumulate && (out_dtype == PQ_I32 || group != 0))
+    return set_error(PQ_EINVAL, "pq_int8_gemm_packed: PQ_ACCUMULATE takes a 16-bit output and per-channel weights");
   if (out_dtype == PQ_I32) {
     if (ldc < N || ldc % 4 != 0 || (uintptr_t)c % 16)
       return set_error(PQ_EALIGN, "pq_int8_gemm_packed: int32 c must be 16-byte aligned with ldc %% 4 == 0");
@@ -897,5 +922,6 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
   args.out_row_idx = out_row_idx;
   args.ldt = ldt; args.ldc = ldc; args.R = (int)R;
   if (group == 32) return dispatch_dtypes<true, kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
+  if (accumulate) return dispatch_dtypes<true, kModeChannel, true>(args, has_lr, lr_dtype, out_dtype, stream);
   return dispatch_dtypes<true, kModeChannel>(args, has_lr, lr_dtype, out_dtype, stream);
 }

@@ -271,10 +271,11 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
                      bias: Optional[torch.Tensor], M: int, N: int, K: int, out_dtype: torch.dtype, *,
                      t: Optional[torch.Tensor] = None, l2t: Optional[torch.Tensor] = None,
                      out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None,
-                     group: int = 0) -> torch.Tensor:
+                     group: int = 0, accumulate: bool = False) -> torch.Tensor:
     """The fused GEMM over packed K64 operands (pq_int8_gemm_packed): xq_p from quant_rows_packed, w_p from
     pack_k64. group 0: w_scale [N]; group 32: w_scale [K/32, N] (group-major). out_dtype torch.int32 returns the
-    raw accumulator."""
+    raw accumulator. accumulate=True (per-channel weights, 16-bit out): out += result in the epilogue, each element
+    rounded as torch's 16-bit add rounds it."""
     assert xq_p.dtype == torch.int8 and w_p.dtype == torch.int8
     _check_cuda(xq_p, s_row, w_p, w_scale, bias, t, l2t, out, out_row_idx)
     assert xq_p.numel() >= packed_rows(M) * K and w_p.numel() >= packed_rows(N) * K
@@ -294,6 +295,7 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
         assert bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == N
     if ori is not None:
         assert ori.shape[0] == M and out is not None, "a scatter needs the destination canvas (out=)"
+    assert out is not None or not accumulate, "accumulate=True adds into out="
     if out is None:
         out = torch.empty((M, N), dtype=out_dtype, device=xq_p.device)
     assert out.dtype == out_dtype and out.dim() == 2 and out.shape[1] == N and out.stride(1) == 1
@@ -306,9 +308,10 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
         R = t.shape[1]
         assert l2t.shape == (N, R), (tuple(l2t.shape), (N, R))
         lr_code, ldt = _lib.dtype_code(t.dtype), t.stride(0)
+    out_code = _lib.dtype_code(out_dtype) | (_lib.PQ_ACCUMULATE if accumulate else 0)
     _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), _lib.ptr(s_row), _lib.ptr(w_scale), group,
                                      _lib.ptr(bias), _lib.ptr(t), ldt, _lib.ptr(l2t), R, lr_code, _lib.ptr(out),
-                                     out.stride(0), _lib.dtype_code(out_dtype), _lib.ptr(ori), M, N, K,
+                                     out.stride(0), out_code, _lib.ptr(ori), M, N, K,
                                      _lib.stream_of(xq_p.device)), "int8_gemm_packed")
     return out
 
@@ -494,9 +497,15 @@ class Int8Linear(nn.Module):
         return out.reshape(*x.shape[:-1], N)
 
     def forward(self, x: torch.Tensor, row_idx: Optional[torch.Tensor] = None,
-                out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
+                out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None,
+                accumulate: bool = False) -> torch.Tensor:
         """y = Linear(x) through quantizer (+ low-rank down) + fused GEMM (deploy/int8_exec.py:382-408).
-        Routed use: ``row_idx`` gathers rows of x (2-D x only), ``out``/``out_row_idx`` scatter into a canvas."""
+        Routed use: ``row_idx`` gathers rows of x (2-D x only), ``out``/``out_row_idx`` scatter into a canvas; their
+        entries must be in range (rows of x, rows of out), which the kernels do not check.
+        ``accumulate=True`` adds the result into ``out`` (2-D, [rows, N]) instead of overwriting it, each element
+        rounded as torch's 16-bit ``out + y`` rounds it: a Linear split along its input sums its halves this way."""
+        if accumulate:
+            assert out is not None, "accumulate=True adds into out="
         if row_idx is None and out is None and out_row_idx is None and self.weight_packed is not None and DIRECT_CALLS:
             y = self._forward_direct(x)
             if y is not None:
@@ -522,24 +531,33 @@ class Int8Linear(nn.Module):
                 t = t.to(x2.dtype)
         t_epi = None if t is None or self.lr_Bt is None else t[:, :self.lr_Bt.shape[1]]
         if t is not None and t_epi is None:
-            return self._forward_lr_after(x2, shape, xq, sx, t, row_idx, out, out_row_idx)
-        if self.weight_packed is not None:
+            return self._forward_lr_after(x2, shape, xq, sx, t, row_idx, out, out_row_idx, accumulate)
+        if self.weight_packed is not None and (not accumulate or not self.group_size):
             if xq is None:
                 xq, sx = quant_rows_packed(x2, row_idx)
             y = int8_gemm_packed(xq, sx, self.weight_packed, self._scale_k(), self.bias, sx.shape[0],
                                  self.out_features, self.in_features, x2.dtype, t=t_epi, l2t=self._lr_bt(x2.dtype),
-                                 out=out, out_row_idx=out_row_idx, group=self.group_size)
+                                 out=out, out_row_idx=out_row_idx, group=self.group_size, accumulate=accumulate)
         else:
-            xq, sx = quant_rows(x2, row_idx)
-            y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, t_epi,
-                      self._lr_bt(x2.dtype), x2.dtype, out, out_row_idx)
+            if xq is None:
+                xq, sx = quant_rows_packed(x2, row_idx) if self.weight_packed is not None else quant_rows(x2, row_idx)
+            if self.weight_packed is not None:   # group-32 weights accumulating: the GEMM's own output, then the add
+                y = int8_gemm_packed(xq, sx, self.weight_packed, self._scale_k(), self.bias, sx.shape[0],
+                                     self.out_features, self.in_features, x2.dtype, t=t_epi,
+                                     l2t=self._lr_bt(x2.dtype), group=self.group_size)
+            else:
+                y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, t_epi,
+                          self._lr_bt(x2.dtype), x2.dtype, None if accumulate else out,
+                          None if accumulate else out_row_idx)
+            if accumulate:
+                return _add_into(out, y, out_row_idx)
         if out is not None or row_idx is not None:
             return y
         return y.reshape(*shape[:-1], self.out_features)
 
-    def _forward_lr_after(self, x2, shape, xq, sx, t, row_idx, out, out_row_idx):
+    def _forward_lr_after(self, x2, shape, xq, sx, t, row_idx, out, out_row_idx, accumulate=False):
         """Ranks above the epilogue's: the GEMM without the low-rank term, then y += t @ lr_B in place
-        (deploy/int8_exec.py:394-407), then the scatter into the canvas if one is given."""
+        (deploy/int8_exec.py:394-407), then the scatter into (or the add to) the canvas if one is given."""
         if xq is None:
             xq, sx = quant_rows_packed(x2, row_idx) if self.weight_packed is not None else quant_rows(x2, row_idx)
         M = sx.shape[0]
@@ -549,6 +567,8 @@ class Int8Linear(nn.Module):
         else:
             y = _gemm(xq, sx, self.weight_int8, self._scale_k(), self.group_size, self.bias, None, None, x2.dtype)
         y.addmm_(t[:, :self.lr_A.shape[1]], self.lr_B.to(y.dtype))
+        if accumulate:
+            return _add_into(out, y, out_row_idx)
         if out is not None:
             if out_row_idx is not None:
                 out.index_copy_(0, out_row_idx.long(), y)
@@ -563,6 +583,16 @@ class Int8Linear(nn.Module):
         g = f"group-{self.group_size}" if self.group_size else "per-channel"
         lr = f", low-rank r={self.lr_A.shape[1]}" if self.lr_A is not None else ""
         return f"in={self.in_features}, out={self.out_features}, int8 {g} W / per-token A{lr} (HIP gfx950)"
+
+
+def _add_into(out: torch.Tensor, y: torch.Tensor, out_row_idx: Optional[torch.Tensor]) -> torch.Tensor:
+    """out[rows] += y with torch's 16-bit add (the accumulate mode where the GEMM's epilogue cannot do it)."""
+    if out_row_idx is None:
+        out[: y.shape[0]].add_(y)
+    else:
+        idx = out_row_idx.long()
+        out.index_copy_(0, idx, out.index_select(0, idx).add_(y))
+    return out
 
 
 # --------------------------------------------------------------------------- model conversion

@@ -67,12 +67,15 @@ def rel_errors(got, ref):
 ELEM_REL, T_STEP, ACC_FLOOR = 1e-2, 2.0 ** -7, 2.0 ** -16
 
 
-def elem_violation(got, ref, t=None, l2=None):
+def elem_violation(got, ref, t=None, l2=None, extra=None):
     """Largest ratio |y - r| / bound over the elements (<= 1 passes). t [M, R] and l2 [R, N] as float arrays (the
-    oracle's low-rank operands), or None without a low-rank branch."""
+    oracle's low-rank operands), or None without a low-rank branch; `extra`, an array added to the bound for a
+    rounding the result carries beyond one layer's (a sum of two rounded layer outputs)."""
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)
     bound = ELEM_REL * np.abs(ref) + ACC_FLOOR * np.abs(ref).max()
     if t is not None:
         bound = bound + T_STEP * (np.abs(np.asarray(t, np.float64)) @ np.abs(np.asarray(l2, np.float64)))
+    if extra is not None:
+        bound = bound + np.asarray(extra, np.float64)
     return float((np.abs(got - ref) / bound).max())

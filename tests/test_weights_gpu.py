@@ -175,3 +175,76 @@ def test_load_method_weights_package(cuda, tmp_path):
         y8 = model.blocks[0].proj_out(x)      # both halves read row-strided views of x
     rel = float((y8.float() - y16.float()).norm() / y16.float().norm())
     assert rel < 2e-2, rel
+
+
+@pytest.mark.parametrize("M,lowrank", [(300, 0), (300, 32), (4352, 32), (65792, 32)])
+def test_split_linear_accumulates_in_epilogue(oracle, cuda, M, lowrank):
+    """The FLUX single-block proj_out split along its input (K = 3072 + 12288 -> N = 3072), both halves Int8Linear:
+    the second half adds its result into the first half's output inside its GEMM epilogue (PQ_ACCUMULATE). That is
+    bit-identical to torch's y0 + y1 of the two halves' outputs; without a low-rank branch it is bit-identical to the
+    oracle's two layers summed with one 16-bit rounding (round(round(y0) + round(y1))), and with one it is within
+    the tolerance of the oracle's fp32 sum, on 104 sampled rows (the last 40 included) at every M: 300 and 4352 run
+    the 128-wide tiles, 65792 (FLUX 4K, 4096^2 image + 256 text tokens) the 256 x 256 tiles."""
+    from conftest import MAX_REL, MEAN_REL, bits, elem_violation, rel_errors
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd import weights
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    K0, K1, N = 3072, 12288, 3072
+    lin = make_linear(K0 + K1, N, 0, True, seed=21).to(torch.bfloat16)
+    split = weights.SplitInLinear(lin.to(cuda), K0)
+    heads = [make_linear(k, N, lowrank, False, seed=30 + h) for h, k in enumerate((K0, K1))]
+    for h, half in enumerate(split.linears):
+        if lowrank:
+            setattr(half, E.LOWRANK_A_ATTR, getattr(heads[h], E.LOWRANK_A_ATTR).to(cuda))
+            setattr(half, E.LOWRANK_B_ATTR, getattr(heads[h], E.LOWRANK_B_ATTR).to(cuda))
+        split.linears[h] = E.Int8Linear(half, device=cuda)
+    x = make_x(M, K0 + K1, seed=M, device=cuda)
+    y = split(x)
+    q0, q1 = split.linears
+    y_sum = q0(x[:, :K0]) + q1(x[:, K0:])
+    assert torch.equal(y, y_sum), "the epilogue's accumulate must round as torch's 16-bit add"
+
+    g = torch.Generator().manual_seed(M)
+    rows = torch.cat([torch.randperm(M - 40, generator=g)[:64], torch.arange(M - 40, M)]).sort().values.to(cuda)
+    xs = x[rows]
+    outs = []
+    for q, sl in ((q0, slice(0, K0)), (q1, slice(K0, K0 + K1))):
+        outs.append(oracle.linear(bits(xs[:, sl].contiguous()), 0, q.weight_int8.cpu().numpy(), q.w_scale.cpu().numpy(),
+                                  None if q.bias is None else q.bias.cpu().numpy(), 0,
+                                  bits(q.lr_A) if lowrank else None, bits(q.lr_B) if lowrank else None))
+    got = bits(y[rows])
+    if not lowrank:
+        both = oracle.to_f32(outs[0]["out"], 0) + oracle.to_f32(outs[1]["out"], 0)
+        assert np.array_equal(got, oracle.from_f32(both, 0))
+        return
+    ref = outs[0]["y"].astype(np.float64) + outs[1]["y"]
+    yf = oracle.to_f32(got, 0)
+    mx, mean = rel_errors(yf, ref)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    t = np.concatenate([oracle.to_f32(o["t"], 0) for o in outs], axis=1)
+    l2 = np.concatenate([oracle.to_f32(bits(q.lr_B), 0) for q in (q0, q1)], axis=0)
+    # the sum carries the 16-bit rounding of each half's output (2^-9 of each, bf16) on top of one layer's bar
+    halves = 2.0 ** -9 * (np.abs(outs[0]["y"].astype(np.float64)) + np.abs(outs[1]["y"]))
+    assert elem_violation(yf, ref, t, l2, extra=halves) <= 1.0
+
+
+def test_accumulate_scatter_and_group32(cuda):
+    """PQ_ACCUMULATE with a routed scatter (canvas[rows] += y, other rows untouched), and Int8Linear's accumulate for
+    group-32 weights (the GEMM's output added by torch): both equal canvas + y computed by torch."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    for group, dt in ((0, torch.bfloat16), (32, torch.float16)):
+        q = E.Int8Linear(make_linear(1280, 640, 0 if group else 32, True, seed=5, dtype=dt), device=cuda,
+                         group_size=group)
+        x = make_x(500, 1280, dt, seed=6, device=cuda)
+        g = torch.Generator().manual_seed(7)
+        ri = torch.randperm(500, generator=g)[:123].to(torch.int32).to(cuda)
+        ori = torch.randperm(900, generator=g)[:123].to(torch.int32).to(cuda)
+        canvas = make_x(900, 640, dt, seed=8, outlier_frac=0.0, device=cuda)
+        expect = canvas.clone()
+        y = q(x, row_idx=ri)
+        expect[ori.long()] = expect[ori.long()] + y
+        q(x, row_idx=ri, out=canvas, out_row_idx=ori, accumulate=True)
+        assert torch.equal(canvas, expect), group
