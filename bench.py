@@ -34,7 +34,7 @@ def main() -> int:
     ap.add_argument("--config", default="c1")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=16384, help="row sample of the CPU baseline")
-    ap.add_argument("--cpu-iters", type=int, default=3)
+    ap.add_argument("--cpu-iters", type=int, default=5)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 3 device-to-device copies of BYTES (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE "
                          "against a plain copy kernel of known size) and exit")
@@ -44,6 +44,9 @@ def main() -> int:
     ap.add_argument("--blaslt", action="store_true",
                     help="only compare the int32-output GEMM with hipBLASLt's (torch._int_mm) on the config's "
                          "operands, like for like, and print one JSON line")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="only time streaming re-reads of buffers from 16 MB to 2 GB (plain and non-temporal loads): "
+                         "where the 256 MB memory-side cache serves a second read; one JSON line")
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only run the register-only MFMA throughput probe (random / constant / zero operands, int8 "
                          "and fp16 MFMA) and print one JSON line")
@@ -73,6 +76,9 @@ def main() -> int:
         return 0
     if args.mfma_ceiling:
         print(json.dumps(mfma_ceiling(dev)), flush=True)
+        return 0
+    if args.read_probe:
+        print(json.dumps(read_probe(dev)), flush=True)
         return 0
     cfg = CONFIGS[args.config]
     if args.blaslt:
@@ -180,6 +186,7 @@ def main() -> int:
     routing = route_bench(dev, not args.no_cpu) if cfg.routed and side else None
     launch = launch_bench(dev) if cfg.group and side else None
     fold = fold_bench(dev, cfg) if cfg.name == "c1" and side else None
+    mix = flux_linear_mix(dev) if cfg.name == "c1" and side else None
 
     res = {
         "metric": METRIC,
@@ -211,7 +218,7 @@ def main() -> int:
             "quantizer_alone": {"kernel": "quant_rows_packed", "us": round(qa_ms * 1e3, 1),
                                 "GBps": round(qa_gbs, 1), "frac_hbm": round(qa_gbs / HBM_PEAK_GBS, 4),
                                 "bytes": f"3 M K + 4 M{' + 4 M (gather list)' if rows is not None else ''}"},
-        } | ({"routing": routing} if routing is not None else {}) | ({"small_m_launch": launch} if launch else {}) | ({"weight_fold": fold} if fold else {}),
+        } | ({"routing": routing} if routing is not None else {}) | ({"small_m_launch": launch} if launch else {}) | ({"weight_fold": fold} if fold else {}) | ({"flux_linear_mix": mix} if mix else {}),
         "roofline": {
             "bound": "mfma",
             "achieved": round(gemm_tops, 2),
@@ -277,12 +284,53 @@ def blaslt_compare(dev, cfg):
     return {"blaslt_compare": res, "int32_equal_to_int_mm": same, "config": cfg.name, "M": cfg.M, "K": cfg.K, "N": cfg.N}
 
 
+def read_probe(dev):
+    """Streaming reads (pyraquant_amd/csrc/probe/mfma_ceiling.hip, pq_probe_read) of one buffer of S bytes, read 6
+    times back to back, each read timed by HIP events: the first read comes from HBM, the later ones from the memory-side
+    cache when S fits it. Plain and non-temporal loads; 2048 workgroups of 256 threads."""
+    import ctypes
+
+    import torch
+
+    from pyraquant_amd import build as B
+
+    lib = ctypes.CDLL(B.PROBE_PATH)
+    lib.pq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                  ctypes.c_void_p]
+    lib.pq_probe_read.restype = ctypes.c_int
+    stream = torch.cuda.current_stream(dev)
+    blocks = 2048
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)   # 1 GiB written between sizes: evicts the cache
+    cases = []
+    for mb in (16, 64, 128, 192, 256, 384, 512, 2048):
+        buf = torch.ones(mb << 20, dtype=torch.uint8, device=dev)
+        for nt in (0, 1):
+            flush.fill_(nt + 1)
+            gbs = []
+            for _ in range(6):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                assert lib.pq_probe_read(ctypes.c_void_p(buf.data_ptr()), buf.numel(), nt, blocks,
+                                         ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream.cuda_stream)) == 0
+                e1.record(stream)
+                torch.cuda.synchronize()
+                gbs.append(buf.numel() / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+            cases.append({"MB": mb, "loads": "nontemporal" if nt else "plain", "first_GBps": round(gbs[0], 1),
+                          "reread_GBps_median": round(sorted(gbs[1:])[2], 1)})
+            print(f"[read-probe] {mb:5d} MB {'nt   ' if nt else 'plain'}: first {gbs[0]:8.1f} GB/s, "
+                  f"re-read {sorted(gbs[1:])[2]:8.1f} GB/s", flush=True)
+        del buf
+    return {"read_probe": cases}
+
+
 def mfma_ceiling(dev):
     """Register-only MFMA loops (pyraquant_amd/csrc/probe/mfma_ceiling.hip) over the whole chip: the throughput the
     matrix cores sustain with no memory traffic at all, for random, constant and zero operands, at 1, 2 and 4 waves
     per SIMD. int8: v_mfma_i32_32x32x32_i8 against 5.0 POP/s; fp16: v_mfma_f32_32x32x16_f16 on the fp16 images of
     int8 codes against 2.5 PFLOP/s; int8 again in 8-wave workgroups, with and without a static issue priority for
-    waves 0-3. Each case: one warm-up launch, then the median of 3 launches timed by HIP events
+    waves 0-3; and the group-32 inner loop (int8 MFMA + convert + fma against two fp16 MFMAs + fma, int8-equivalent
+    ops). Each case: one warm-up launch, then the median of 3 launches timed by HIP events
     on the launch stream (about 20 ms each)."""
     import ctypes
 
@@ -305,12 +353,14 @@ def mfma_ceiling(dev):
     plan = ((0, "i32_32x32x32_i8", 65536, INT8_PEAK_TOPS, 4, ("random", "constant", "zero"), (1, 2, 4)),
             (1, "f32_32x32x16_f16", 32768, INT8_PEAK_TOPS / 2, 4, ("random", "constant", "zero"), (1, 2, 4)),
             (2, "i32_32x32x32_i8 8-wave WG", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)),
-            (3, "i32_32x32x32_i8 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)))
+            (3, "i32_32x32x32_i8 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)),
+            (4, "group-32 loop: i8 MFMA + cvt + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2, 4)),
+            (5, "group-32 loop: 2 f16 MFMA + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2, 4)))
     for kind, name, per_inst, peak, wpb, patterns, wps_list in plan:
         for pattern in patterns:
             c = codes[pattern]
             # int8: the bytes themselves; fp16: 8 codes per 16-byte fragment as fp16 values (exact)
-            src = (c[: 16 * 64 * 16].to(torch.int8) if kind != 1 else c[: 16 * 64 * 8].to(torch.float16)).to(dev)
+            src = (c[: 16 * 64 * 16].to(torch.int8) if kind not in (1, 5) else c[: 16 * 64 * 8].to(torch.float16)).to(dev)
             for wps in wps_list:
                 blocks, iters = 256 * wps * 4 // wpb, 100000 // wps
                 call = lambda: lib.pq_probe_mfma(kind, ctypes.c_void_p(src.data_ptr()), blocks, iters,
@@ -325,7 +375,7 @@ def mfma_ceiling(dev):
                     torch.cuda.synchronize()
                     ms.append(e0.elapsed_time(e1))
                 t = sorted(ms)[1] * 1e-3
-                ops = float(blocks) * wpb * iters * 8 * per_inst
+                ops = float(blocks) * wpb * iters * 8 * per_inst   # kinds 4, 5: 2 groups x 4 tiles per iteration
                 rate = ops / t / 1e12
                 cases.append({"mfma": name, "operands": pattern, "waves_per_simd": wps, "ms": round(t * 1e3, 3),
                               "TOPS": round(rate, 1), "frac_of_peak": round(rate / peak, 4)})
@@ -494,8 +544,23 @@ def route_bench(dev, with_cpu: bool):
     return res
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo, what lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(cfg, lin, rows: int, iters: int):
-    """The reference's torch CPU path (oracle/torch_ref.py) on the first `rows` rows of the same layer."""
+    """The reference's torch CPU path (oracle/torch_ref.py) on the first `rows` rows of the same layer: median of
+    `iters` timed calls after one warm-up, all host threads torch may use."""
     import torch
 
     from oracle import torch_ref
@@ -511,15 +576,37 @@ def cpu_baseline(cfg, lin, rows: int, iters: int):
     A = getattr(lin, LOWRANK_A_ATTR, None)
     B = getattr(lin, LOWRANK_B_ATTR, None)
     torch_ref.int8_linear(x, wq, ws, b, A, B)        # warm-up
-    t0 = time.perf_counter()
+    times = []
     for _ in range(iters):
+        t0 = time.perf_counter()
         torch_ref.int8_linear(x, wq, ws, b, A, B)
-    dt = (time.perf_counter() - t0) / iters
+        times.append(time.perf_counter() - t0)
+    dt = sorted(times)[len(times) // 2]
     ops = 2.0 * rows * cfg.N * cfg.K
     return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": torch.get_num_threads(), "kind": "port",
+            "cpu_model": _cpu_model(),
             "sample": f"{rows} of {cfg.M} rows of {cfg.name} (K={cfg.K}, N={cfg.N}), torch CPU quantize + "
-                      f"_int_mm + dequant + low-rank, mean of {iters} after 1 warm-up; "
-                      f"{dt * 1e3:.1f} ms per sample"}
+                      f"_int_mm + dequant + low-rank, median of {iters} after 1 warm-up; "
+                      f"{dt * 1e3:.1f} ms per sample (all: {', '.join(f'{t * 1e3:.0f}' for t in times)} ms)"}
+
+
+def flux_linear_mix(dev):
+    """The reference's own per-image micro-benchmark (deploy/int8_exec.py:539-571, run here by
+    int8_exec.selftest_and_bench): for each token count M the four FLUX token-level Linear shapes, bf16 F.linear
+    against Int8Linear, summed with the per-image layer counts of FLUX_TOKEN_SHAPES (342 layers)."""
+    import contextlib
+
+    from pyraquant_amd import int8_exec as E
+
+    with contextlib.redirect_stdout(sys.stderr):   # its progress lines; stdout carries the one JSON line
+        res = E.selftest_and_bench(Ms=(4352, 16640, 33744, 65792), iters=10)
+    out = {}
+    for M, r in res["per_M"].items():
+        out[M] = {k: r[k] for k in ("bf16_ms", "int8_fused_ms", "quant_ms", "gemm_fused_ms", "speedup_fused_vs_bf16")}
+        out[M]["per_shape_int8_ms"] = {k: v["int8_fused_ms"] for k, v in r["per_shape"].items()}
+    return {"per_M": out, "selftest": res["selftest"],
+            "note": "ms per image for the 342 token-level Linears (per-shape mean x layer count); bf16 = torch F.linear "
+                    "(hipBLASLt), int8 = Int8Linear.forward without low rank, as the reference's benchmark"}
 
 
 if __name__ == "__main__":

@@ -432,15 +432,6 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
   const __amdgpu_buffer_rsrc_t rs_x =
       __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, (int)(x_rows * ldx * 2), kBufferWord3);
 
-  // l1t fragments of this wave's slice: lf[h][2 c + e] = l1t[16 h + r][k0 + 64 c + 16 g + 8 e .. + 8]
-  v4u lf[2][NS];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int i = 0; i < NS; ++i)
-      lf[h][i] = *reinterpret_cast<const v4u*>(l1t + (int64_t)(16 * h + r) * K + k0 + 64 * (i >> 1) + 16 * g +
-                                               8 * (i & 1));
-
   // DMA of batch b: wave w copies rows (16 / W) w .. + 16 / W - 1, CHUNKS pieces each (rows past M: out of range,
   // zeros).
   // Source rows come from uniform (scalar) reads of the gather list, so no vector load joins the vmcnt queue.
@@ -469,6 +460,17 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
   dma();
 #pragma unroll
   for (int j = 0; j < 16 / W; ++j) xoff[j] = row_off(b + G, j);
+  // The first batch's DMA is issued before the l1t slice is loaded: its HBM latency then overlaps the l1t reads
+  // instead of queueing behind them (at small M every workgroup runs a single batch, so nothing else hides it).
+  __builtin_amdgcn_sched_barrier(0);
+  // l1t fragments of this wave's slice: lf[h][2 c + e] = l1t[16 h + r][k0 + 64 c + 16 g + 8 e .. + 8]
+  v4u lf[2][NS];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+      lf[h][i] = *reinterpret_cast<const v4u*>(l1t + (int64_t)(16 * h + r) * K + k0 + 64 * (i >> 1) + 16 * g +
+                                               8 * (i & 1));
   for (; b < nbatch; b += G) {
     // The DMA of batch b is followed by the previous batch's stores; loads and stores are not guaranteed to
     // retire in issue order relative to each other, so wait for everything.
@@ -545,6 +547,178 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
       for (int w = 1; w < W; ++w) {
         v0 = v0 + red[w][mr][rr];
         v1 = v1 + red[w][mr][rr + 1];
+      }
+      if (mo < M) *reinterpret_cast<uint32_t*>(t + mo * ldt + rr) = pack2<DT>(v0, v1);
+    }
+  }
+}
+
+// ---- fused quantizer + low-rank down-projection for wide rows (K = 4096 .. 12288) ---------------------------------
+// The same results as quant_lowrank_kernel (codes and scales of pq_quant_rows_packed, t = x @ L1 rounded to 16 bits)
+// for rows too wide for its LDS staging (c2a: K = 12288, a 16-row batch is 384 KB). x is read from HBM once: a
+// re-read of a batch runs at HBM speed even when the memory-side cache holds it, so reading twice costs twice.
+// One workgroup of 8 waves per CU, persistent over batches of 16 rows; wave w holds rows 2 w and 2 w + 1 of the batch
+// whole in registers (NCH 16-byte chunks per lane per row, the row-per-wave load pattern of quant_rows_vec_kernel).
+// Per batch: the absmax and scale of each row from the registers (a wave reduction; the IEEE steps of
+// quant_rows_vec_kernel); then for each 512-wide K slab e:
+//   a. the wave writes its two rows' chunk e into the x slab buffer (16 rows, double buffered);
+//   c. quantizes chunk e and stores its codes (packed K64);
+//   -- barrier (the x slab is complete, and the L1^T slab e, DMA'd one slab ahead, has landed) --
+//   b. issues the LDS-DMA of the L1^T slab e + 1 (32 rows of 1 KB, double buffered);
+//   d. reads its 64-wide share of slab e for all 16 rows and the matching L1^T fragments (LDS) and runs
+//      v_mfma_f32_16x16x32 into its t partial.
+// The 8 waves' t partials are summed in LDS in wave order, (..(p0 + p1) ..) + p7, and rounded to 16 bits.
+// Batches are software-pipelined through the registers: after chunk e of batch b is in LDS and quantized, the wave
+// loads chunk e of its next batch into the same registers, so the next rows stream in under this batch's work.
+// Ordering: the L1^T DMA of slab e + 1 is issued after barrier e, when every wave has read that buffer's previous slab
+// (e - 1); it must land before barrier e + 1, and the only vector-memory instructions issued after it are slab e + 1's
+// two code stores and two next-batch loads, hence vmcnt(4) there (vector-memory instructions retire in issue order).
+// Past the last batch the next-batch loads read this batch's rows again (discarded), which keeps that count exact.
+constexpr int kWideWaves = 8;                 // waves per workgroup, two rows each: batches of 16 rows
+constexpr int kWideSlab = 512;                // K elements per slab
+constexpr int kWidePitch = 2 * kWideSlab + 16;   // LDS row pitch: consecutive rows 16 bytes apart in the bank window
+constexpr int kWideRedPitch = 36;             // floats per row of the partial-sum buffer
+
+template <int DT, int NCH>   // NCH = K / 512: 16-byte chunks per lane per row, and slabs
+__global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t M, const int32_t* __restrict__ row_idx,
+    const uint16_t* __restrict__ l1t, int8_t* __restrict__ qp, float* __restrict__ s, uint16_t* __restrict__ t,
+    int64_t ldt, int nbatch) {
+  constexpr int K = 512 * NCH;
+  constexpr int KW = kWideSlab / kWideWaves;   // 64: each wave's share of a slab, two MFMA K steps
+  // double buffers as separate arrays, so that the compiler can tell an LDS read of one buffer from a pending
+  // LDS-DMA into the other (it waits for every DMA that may alias a read)
+  __shared__ __attribute__((aligned(1024))) uint8_t lbuf0[32 * kWidePitch], lbuf1[32 * kWidePitch];   // L1^T slabs
+  __shared__ __attribute__((aligned(16))) uint8_t xbuf0[16 * kWidePitch], xbuf1[16 * kWidePitch];     // x slabs
+  __shared__ __attribute__((aligned(16))) float red[kWideWaves][16][kWideRedPitch];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // MFMA 16x16x32 operands: lane l feeds A row (L1^T row) and B column (batch row) l % 16, K group l / 16
+  const int nr = lane & 15, kg = lane >> 4;
+  const __amdgpu_buffer_rsrc_t rs_l =
+      __builtin_amdgcn_make_buffer_rsrc((void*)l1t, (short)0, 32 * K * 2, kBufferWord3);
+  // L1^T slab e -> lbuf[e & 1]: wave w copies rows 4 w .. 4 w + 3, one 1 KB LDS-DMA each; the slab's offset rides
+  // the scalar offset operand, so the per-lane offsets stay four registers
+  const int voff_l = 4 * wave * K * 2 + lane * 16;
+  auto dma_l = [&](int e) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_l, (lds_void_t*)((e & 1 ? lbuf1 : lbuf0) + (4 * wave + i) * kWidePitch), 16,
+                                               voff_l + i * K * 2, e * kWideSlab * 2, 0, 0);
+  };
+
+  // Row rho of this wave in batch bb: its source row in x (row 0 for a padding row past M, whose loads are
+  // harmless and whose data is cleared before use). Wave-uniform: the row bases stay in scalar registers and each
+  // lane adds its own 16-byte offset.
+  auto src_row = [&](int bb, int rho) -> const v4u* {
+    const int64_t m = (int64_t)bb * 16 + 2 * wave + rho;
+    const int64_t src = m >= M ? 0 : (row_idx ? (int64_t)row_idx[m] : m);
+    return reinterpret_cast<const v4u*>(x + src * ldx);
+  };
+  // this lane's byte offset inside a row's packed K64 codes, for the rows 2 w (rho = 0) and 2 w + 1 of a batch
+  int qlane[2];
+#pragma unroll
+  for (int rho = 0; rho < 2; ++rho)
+    qlane[rho] = (lane >> 3) * 1024 + ((((lane >> 1) & 3) ^ k64_swz(2 * wave + rho)) << 4) + (lane & 1) * 8;
+  v4u v[2][NCH];
+  if (blockIdx.x < nbatch) {
+#pragma unroll
+    for (int rho = 0; rho < 2; ++rho) {
+      const v4u* xr = src_row(blockIdx.x, rho);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) v[rho][c] = __builtin_nontemporal_load(xr + c * 64 + lane);
+    }
+  }
+  for (int b = blockIdx.x; b < nbatch; b += gridDim.x) {
+    const int bn = b + gridDim.x;   // the next batch (past the end: this batch's rows again, loaded and discarded)
+    int64_t mrow[2];
+    const v4u* xn[2];
+#pragma unroll
+    for (int rho = 0; rho < 2; ++rho) {
+      mrow[rho] = (int64_t)b * 16 + 2 * wave + rho;
+      xn[rho] = src_row(bn < nbatch ? bn : b, rho);
+      if (mrow[rho] >= M) {   // a padding row: its codes must be zero
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) v[rho][c] = v4u{0u, 0u, 0u, 0u};
+      }
+    }
+    dma_l(0);   // lands before slab 0's barrier: only that slab's code stores and next-batch loads come after it
+    float sc[2], rc[2];
+#pragma unroll
+    for (int rho = 0; rho < 2; ++rho) {
+      us2 mx2 = {0, 0};
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, v[rho][c].x & 0x7fff7fffu));
+        mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, v[rho][c].y & 0x7fff7fffu));
+        mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, v[rho][c].z & 0x7fff7fffu));
+        mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(us2, v[rho][c].w & 0x7fff7fffu));
+      }
+      const uint32_t mx = wave_max_u32(mx2.x > mx2.y ? mx2.x : mx2.y);
+      const float a = fmaxf(absmax_from_bits<DT>(mx), 1e-8f);
+      sc[rho] = __fdiv_rn(a, 127.0f);
+      rc[rho] = __fdiv_rn(1.0f, sc[rho]);
+    }
+    // packed K64 rows of the batch: block row b, row 2 w + rho inside it (k64_offset, split into the wave-uniform
+    // part and qlane)
+    int8_t* const qbatch = qp + (int64_t)b * (K / 64) * 1024 + 2 * wave * 64;
+    v4f acc[2] = {v4f{}, v4f{}};   // t partial of this wave's K shares: D[r = 16 h + 4 kg + i][batch row nr]
+#pragma unroll
+    for (int e = 0; e < NCH; ++e) {
+      uint8_t* const xs = e & 1 ? xbuf1 : xbuf0;
+      const uint8_t* const ls = e & 1 ? lbuf1 : lbuf0;
+#pragma unroll
+      for (int rho = 0; rho < 2; ++rho)
+        *reinterpret_cast<v4u*>(xs + (2 * wave + rho) * kWidePitch + lane * 16) = v[rho][e];
+      // codes of chunk e (padding rows past M hold zeros and quantize to zero codes): K elements 512 e + 8 lane ..
+      // sit 8 packed blocks (8 KB) after those of chunk e - 1
+#pragma unroll
+      for (int rho = 0; rho < 2; ++rho)
+        *reinterpret_cast<v2u*>(qbatch + rho * 64 + e * 8192 + qlane[rho]) = quant_chunk<DT>(v[rho][e], sc[rho], rc[rho]);
+      // chunk e of the next batch into the registers just freed
+#pragma unroll
+      for (int rho = 0; rho < 2; ++rho) v[rho][e] = __builtin_nontemporal_load(xn[rho] + e * 64 + lane);
+      wait_vmcnt<4>();                      // this wave's DMA of L1^T slab e has landed (2 stores, 2 loads after it)
+      __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's x slab writes are done
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();         // both slabs complete; every wave is done with slab e - 1
+      __builtin_amdgcn_sched_barrier(0);
+      if (e + 1 < NCH) dma_l(e + 1);
+#pragma unroll
+      for (int ks = 0; ks < KW / 32; ++ks) {
+        const int kk = wave * KW + ks * 32 + kg * 8;   // K offset inside the slab
+        const v4u bf = *reinterpret_cast<const v4u*>(xs + nr * kWidePitch + kk * 2);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const v4u af = *reinterpret_cast<const v4u*>(ls + (16 * h + nr) * kWidePitch + kk * 2);
+          if constexpr (DT == PQ_BF16)
+            acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, af), __builtin_bit_cast(v8bf, bf),
+                                                            acc[h], 0, 0, 0);
+          else
+            acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, af), __builtin_bit_cast(v8h, bf),
+                                                           acc[h], 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) *reinterpret_cast<v4f*>(&red[wave][nr][16 * h + 4 * kg]) = acc[h];
+    if (lane == 0) {
+#pragma unroll
+      for (int rho = 0; rho < 2; ++rho)
+        if (mrow[rho] < M) s[mrow[rho]] = sc[rho];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();   // every wave's partials are in red (and every wave is done with the last slabs)
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < 256) {
+      const int n = tid >> 4, rr = (tid & 15) * 2;
+      const int64_t mo = (int64_t)b * 16 + n;
+      float v0 = red[0][n][rr], v1 = red[0][n][rr + 1];
+#pragma unroll
+      for (int w = 1; w < kWideWaves; ++w) {
+        v0 = v0 + red[w][n][rr];
+        v1 = v1 + red[w][n][rr + 1];
       }
       if (mo < M) *reinterpret_cast<uint32_t*>(t + mo * ldt + rr) = pack2<DT>(v0, v1);
     }
@@ -693,6 +867,27 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
                      (row_idx || x_rows >= M) && x_rows * ldx * 2 + 2 * K <= 0x3fffffffLL &&
                      (uintptr_t)x % 16 == 0 && (uintptr_t)l1t % 16 == 0 && (uintptr_t)t % 4 == 0 &&
                      (uintptr_t)qp % 16 == 0 && (x_dtype == PQ_BF16 || x_dtype == PQ_F16);
+  // wide rows: one read of x through registers (quant_lowrank_wide_kernel)
+  const bool wide = !fused && R == 32 && K % 2048 == 0 && K >= 4096 && K <= 12288 && ldx >= K && ldx % 8 == 0 &&
+                    ldt >= R && ldt % 2 == 0 && (row_idx || x_rows >= M) && (uintptr_t)x % 16 == 0 &&
+                    (uintptr_t)l1t % 16 == 0 && (uintptr_t)t % 4 == 0 && (uintptr_t)qp % 16 == 0 &&
+                    (x_dtype == PQ_BF16 || x_dtype == PQ_F16);
+  if (wide) {
+    const int nbatch = (int)((M + 15) / 16);
+    const dim3 grid((unsigned)std::min(nbatch, 256));
+    const uint16_t* xp = static_cast<const uint16_t*>(x);
+    const uint16_t* lp = static_cast<const uint16_t*>(l1t);
+    uint16_t* tp = static_cast<uint16_t*>(t);
+#define PQ_QWCASE(D, NCH)                                                                                      \
+    if (x_dtype == D && K == 512 * NCH) {                                                                      \
+      hipLaunchKernelGGL((quant_lowrank_wide_kernel<D, NCH>), grid, dim3(64 * kWideWaves), 0, stream, xp, ldx, M, \
+                         row_idx, lp, qp, s, tp, ldt, nbatch);                                                 \
+      return check_launch("quant_rows_lowrank");                                                               \
+    }
+    PQ_QWCASE(PQ_BF16, 8) PQ_QWCASE(PQ_BF16, 12) PQ_QWCASE(PQ_BF16, 16) PQ_QWCASE(PQ_BF16, 20) PQ_QWCASE(PQ_BF16, 24)
+    PQ_QWCASE(PQ_F16, 8) PQ_QWCASE(PQ_F16, 12) PQ_QWCASE(PQ_F16, 16) PQ_QWCASE(PQ_F16, 20) PQ_QWCASE(PQ_F16, 24)
+#undef PQ_QWCASE
+  }
   if (!fused) {
     const int st = pq_quant_rows_packed(x, x_dtype, M, K, ldx, row_idx, qp, s, stream);
     if (st != PQ_OK) return st;

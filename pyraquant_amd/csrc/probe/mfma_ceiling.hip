@@ -11,6 +11,10 @@
 //   kind 2: kind 0 in workgroups of 8 waves (two per SIMD), all at the default issue priority
 //   kind 3: kind 2 with waves 0-3 raised to issue priority 1 (s_setprio) for the whole kernel: on each SIMD the
 //           high-priority wave issues its MFMAs back to back and the other wave issues only when it stalls
+//   kind 4: the group-32 inner loop on int8 MFMAs: per 32-wide K group and 32 x 32 tile, one
+//           v_mfma_i32_32x32x32_i8 from zero, then acc = fma(scale, (float)partial, acc) on the 16 values per lane
+//   kind 5: the same group on fp16 MFMAs: two v_mfma_f32_32x32x16_f16 (the partial arrives in fp32, exact for
+//           int8 codes), then the 16 fmas; kinds 4 and 5 count 65536 int8-equivalent ops per group and tile
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -34,7 +38,40 @@ __global__ __launch_bounds__(512) void mfma_ceiling_kernel(const v4i* __restrict
     a[i] = src[i * 64 + lane];
     b[i] = src[(8 + i) * 64 + lane];
   }
-  if constexpr (KIND != 1) {
+  if constexpr (KIND == 4 || KIND == 5) {
+    // 2 x 2 tiles of fp32 accumulators; the group scales rotate through 8 registers per lane
+    float sc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sc[i] = 1.0f + 1e-3f * (float)((lane + i) & 7);
+    v16f acc[4] = {v16f{}, v16f{}, v16f{}, v16f{}};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float sg = sc[(4 * g + t) & 7];
+          if constexpr (KIND == 4) {
+            const v16i part = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[2 * g + (t >> 1)], b[4 * g + (t & 1)], v16i{}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(sg, (float)part[r], acc[t][r]);
+          } else {
+            v16f part = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a[4 * g + (t >> 1)]),
+                                                               __builtin_bit_cast(v8h, b[4 * g + (t & 1)]), v16f{}, 0, 0, 0);
+            part = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a[4 * g + 2 + (t >> 1)]),
+                                                          __builtin_bit_cast(v8h, b[4 * g + 2 + (t & 1)]), part, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(sg, part[r], acc[t][r]);
+          }
+        }
+      }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += acc[j][r];
+    sink[blockIdx.x * blockDim.x + threadIdx.x] = __float_as_int(s);
+  } else if constexpr (KIND != 1) {
     v16i acc[4] = {v16i{}, v16i{}, v16i{}, v16i{}};
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
@@ -65,7 +102,39 @@ __global__ __launch_bounds__(512) void mfma_ceiling_kernel(const v4i* __restrict
   }
 }
 
+// Streaming read of `n16` 16-byte chunks, grid-stride, plain (NT = 0) or non-temporal (NT = 1) loads; the XOR of
+// everything read goes to sink so the loads stay.
+template <int NT>
+__global__ __launch_bounds__(256) void read_probe_kernel(const v4i* __restrict__ src, int64_t n16,
+                                                         int* __restrict__ sink) {
+  v4i x = v4i{0, 0, 0, 0};
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += 4 * stride) {
+    v4i v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = i + u * stride;
+      if (j < n16) v[u] = NT ? __builtin_nontemporal_load(src + j) : src[j];
+      else v[u] = v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x ^= v[u];
+  }
+  sink[blockIdx.x * blockDim.x + threadIdx.x] = x.x ^ x.y ^ x.z ^ x.w;
+}
+
 }  // namespace
+
+// Streaming read of `bytes` (a multiple of 16) from src over `blocks` workgroups of 256 threads (sink: blocks * 256
+// ints), plain or non-temporal loads: how fast a buffer of a given size is read back, HBM or memory-side cache.
+extern "C" int pq_probe_read(const void* src, int64_t bytes, int nt, int blocks, int* sink, hipStream_t stream) {
+  if (!src || !sink || bytes < 16 || bytes % 16 || blocks < 1) return -1;
+  if (nt) hipLaunchKernelGGL(read_probe_kernel<1>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
+                             bytes / 16, sink);
+  else hipLaunchKernelGGL(read_probe_kernel<0>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
+                          bytes / 16, sink);
+  return (int)hipGetLastError();
+}
 
 // Runs the probe once: `blocks` workgroups of 4 waves (8 for kinds 2 and 3), `iters` x 8 MFMAs per wave, operands from `src` (16 x 64
 // fragments of 16 bytes). Returns 0 or a HIP error code; the kernel time is left to the caller's events.
@@ -82,6 +151,12 @@ extern "C" int pq_probe_mfma(int kind, const void* src, int blocks, int iters, i
                        iters, sink);
   } else if (kind == 3) {
     hipLaunchKernelGGL(mfma_ceiling_kernel<3>, dim3(blocks), dim3(512), 0, stream, static_cast<const v4i*>(src),
+                       iters, sink);
+  } else if (kind == 4) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel<4>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
+                       iters, sink);
+  } else if (kind == 5) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel<5>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
                        iters, sink);
   } else {
     return -1;

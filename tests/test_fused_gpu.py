@@ -3,8 +3,9 @@
 * packed codes and scales bit-identical to pq_quant_rows_packed on the same rows (which the quantizer tests pin
   against the oracle);
 * t within bf16 rounding of the float64 product and within the build's tolerance of the oracle's fp32 result;
-* shapes the fused kernel does not take (K = 4096 .. 15360, K outside its list, R != 32) run the two kernels: the
-  same bar, and exactly what the two separate entry points give.
+* K = 4096 .. 12288 in steps of 2048 (c2a's 12288) run the wide kernel, which holds rows in registers: the same bar;
+* other shapes (K outside both lists, R != 32) run the two kernels: the same bar, and exactly what the two separate
+  entry points give.
 """
 import numpy as np
 import pytest
@@ -34,7 +35,7 @@ def _check_t(oracle, t, x_rows, l1, dtype):
 @pytest.mark.parametrize("M,K", [(1, 3072), (16, 3072), (17, 3072), (1000, 1280), (4099, 3072), (300, 2048),
                                  (65, 2560), (33, 1024), (20000, 3072),
                                  (1, 12288), (7, 12288), (1001, 12288), (37, 4096), (100, 5120), (50, 6144),
-                                 (23, 15360), (9000, 12288)])
+                                 (23, 15360), (9000, 12288), (4111, 8192), (17, 10240)])
 def test_quant_rows_lowrank_fused(oracle, cuda, dtype, M, K):
     from pyraquant_amd import int8_exec as E
     from pyraquant_amd.workloads import make_x
@@ -72,9 +73,10 @@ def test_quant_rows_lowrank_gather_view(oracle, cuda):
     _check_t(oracle, t, x.cpu()[idx.long()], l1, torch.bfloat16)
 
 
-@pytest.mark.parametrize("M,K,R", [(100, 12288, 32), (70, 640, 32), (300, 3072, 64), (40, 12288, 64)])
+@pytest.mark.parametrize("M,K,R", [(100, 5120, 32), (70, 640, 32), (300, 3072, 64), (40, 12288, 64),
+                                   (50, 15360, 32)])
 def test_quant_rows_lowrank_fallback(cuda, M, K, R):
-    """Shapes outside the fused kernel's set run the two kernels: identical to calling them one after the other."""
+    """Shapes outside the fused kernels' sets run the two kernels: identical to calling them one after the other."""
     from pyraquant_amd import int8_exec as E
     from pyraquant_amd.workloads import make_x
 
@@ -87,7 +89,7 @@ def test_quant_rows_lowrank_fallback(cuda, M, K, R):
 
 
 def test_quant_rows_lowrank_wide_gather_view(oracle, cuda):
-    """K = 12288 (the two-kernel path) through a gather with duplicates and a row-slice view (ldx = K + 512): codes
+    """K = 12288 (the wide kernel) through a gather with duplicates and a row-slice view (ldx = K + 512): codes
     and scales bit-identical to the packed quantizer's, t within bf16 rounding of the float64 product."""
     from pyraquant_amd import int8_exec as E
     from pyraquant_amd.workloads import make_x

@@ -516,3 +516,35 @@ def test_planted_mistakes_are_caught(oracle):
     w = torch.randint(-127, 128, (64, 64), generator=g, dtype=torch.int8)
     transposed = a.numpy().astype(np.int64) @ w.numpy().astype(np.int64)
     assert not np.array_equal(transposed, torch._int_mm(a, w.t()).numpy())
+
+
+def test_pack_k64_layout_spot_checks(oracle):
+    """The numpy packed-K64 restatement against the layout's definition (include/pyraquant_amd.h), element by element
+    on random positions, computed independently: byte (r, k) of X lives at block (r // 16, k // 64), row r % 16, slot
+    ((k // 16) % 4) ^ swz(r % 16), byte k % 16; swz taken from its bit formula. Plus the round trip through
+    unpack_k64, zero padding rows, and a swizzle check that a plain (unswizzled) layout would fail."""
+    rng = np.random.default_rng(5)
+    R, K = 37, 192
+    x = rng.integers(-128, 128, size=(R, K), dtype=np.int8)
+    p = oracle.pack_k64(x)
+    KT = K // 64
+    assert p.shape == (((R + 15) // 16) * 16 * K,)
+
+    def swz(r):
+        b2, b1, b3 = (r >> 2) & 1, (r >> 1) & 1, (r >> 3) & 1
+        return b2 | ((b1 ^ b3) << 1)
+
+    assert [swz(r) for r in range(16)] == [int(v) for v in oracle.k64_swz(np.arange(16))]
+    for _ in range(2000):
+        r, k = int(rng.integers(R)), int(rng.integers(K))
+        off = ((r // 16) * KT + k // 64) * 1024 + (r % 16) * 64 + ((((k // 16) % 4) ^ swz(r % 16)) << 4) + k % 16
+        assert p[off] == x[r, k], (r, k)
+    assert np.array_equal(oracle.unpack_k64(p, R, K), x)
+    pad = p.reshape(-1, KT, 16, 64)[-1, :, R % 16:]          # rows 37..47 of the last block
+    assert not pad.any()
+    # the swizzle is not the identity on every row: an unswizzled copy differs
+    plain = np.zeros_like(p).reshape(-1, KT, 16, 64)
+    xp = np.zeros((((R + 15) // 16) * 16, K), np.int8)
+    xp[:R] = x
+    plain[:] = xp.reshape(-1, 16, KT, 64).transpose(0, 2, 1, 3)
+    assert not np.array_equal(plain.reshape(-1), p)
