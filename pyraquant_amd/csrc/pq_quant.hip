@@ -17,6 +17,7 @@
 #include "pq_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -471,10 +472,17 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
     for (int i = 0; i < NS; ++i)
       lf[h][i] = *reinterpret_cast<const v4u*>(l1t + (int64_t)(16 * h + r) * K + k0 + 64 * (i >> 1) + 16 * g +
                                                8 * (i & 1));
-  for (; b < nbatch; b += G) {
-    // The DMA of batch b is followed by the previous batch's stores; loads and stores are not guaranteed to
-    // retire in issue order relative to each other, so wait for everything.
-    wait_vmcnt<0>();
+  // One batch. The first batch's DMA is followed only by the l1t loads (4 NC of them), which may stay in flight: the
+  // low-rank MFMAs that need them come after the codes, so the l1t reads land under that work (at small M every
+  // workgroup runs one batch and nothing else would hide them). The first batch is peeled off the loop, so that the
+  // compiler's wait for the l1t registers sits at those MFMAs rather than before the loop. Later DMAs are followed
+  // by the previous batch's stores, a count that differs between waves, so those waits are for everything.
+  auto batch = [&](int b, auto first) {
+    if constexpr (decltype(first)::value) {
+      wait_vmcnt<4 * NC>();
+    } else {
+      wait_vmcnt<0>();
+    }
     __syncthreads();   // every wave's DMA of batch b has landed
 #pragma unroll
     for (int i = 0; i < NS; ++i) xv[i] = *reinterpret_cast<const v4u*>(xrow + 128 * (i >> 1) + 16 * (i & 1));
@@ -501,19 +509,6 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
       mx = mx > o ? mx : o;
     }
     if (g == 0) amax_l[wave][r] = mx;
-    // low rank: partial t over the slice (independent of the scale)
-    v4f acc[2] = {v4f{}, v4f{}};
-#pragma unroll
-    for (int i = 0; i < NS; ++i)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if constexpr (DT == PQ_BF16)
-          acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, lf[h][i]),
-                                                          __builtin_bit_cast(v8bf, xv[i]), acc[h], 0, 0, 0);
-        else
-          acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, lf[h][i]),
-                                                         __builtin_bit_cast(v8h, xv[i]), acc[h], 0, 0, 0);
-      }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();   // amax_l complete (LDS only: the DMA of the next batch stays in flight)
@@ -532,6 +527,19 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
       *reinterpret_cast<v4u*>(qp + k64_offset(m, k0 + 64 * c + 16 * g, K / 64)) = v4u{lo.x, lo.y, hi.x, hi.y};
     }
     if (wave == 0 && g == 0 && m < M) s[m] = sc;
+    // low rank: partial t over the slice, after the codes so that the first batch's l1t loads land under them
+    v4f acc[2] = {v4f{}, v4f{}};
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if constexpr (DT == PQ_BF16)
+          acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, lf[h][i]),
+                                                          __builtin_bit_cast(v8bf, xv[i]), acc[h], 0, 0, 0);
+        else
+          acc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, lf[h][i]),
+                                                         __builtin_bit_cast(v8h, xv[i]), acc[h], 0, 0, 0);
+      }
     // D[rr][m]: lane holds m = r and rr = 16 h + 4 g + (0..3)
 #pragma unroll
     for (int h = 0; h < 2; ++h) *reinterpret_cast<v4f*>(&red[wave][r][16 * h + 4 * g]) = acc[h];
@@ -550,7 +558,9 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
       }
       if (mo < M) *reinterpret_cast<uint32_t*>(t + mo * ldt + rr) = pack2<DT>(v0, v1);
     }
-  }
+  };
+  if (b < nbatch) batch(b, std::true_type{});
+  for (b += G; b < nbatch; b += G) batch(b, std::false_type{});
 }
 
 // ---- fused quantizer + low-rank down-projection for wide rows (K = 4096 .. 12288) ---------------------------------
