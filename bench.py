@@ -330,7 +330,7 @@ def mfma_ceiling(dev):
     per SIMD. int8: v_mfma_i32_32x32x32_i8 against 5.0 POP/s; fp16: v_mfma_f32_32x32x16_f16 on the fp16 images of
     int8 codes against 2.5 PFLOP/s; int8 again in 8-wave workgroups, with and without a static issue priority for
     waves 0-3; and the group-32 inner loop (int8 MFMA + convert + fma against two fp16 MFMAs + fma, int8-equivalent
-    ops). Each case: one warm-up launch, then the median of 3 launches timed by HIP events
+    ops), plain and with the priority split. Each case: one warm-up launch, then the median of 3 launches timed by HIP events
     on the launch stream (about 20 ms each)."""
     import ctypes
 
@@ -355,12 +355,16 @@ def mfma_ceiling(dev):
             (2, "i32_32x32x32_i8 8-wave WG", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)),
             (3, "i32_32x32x32_i8 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)),
             (4, "group-32 loop: i8 MFMA + cvt + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2, 4)),
-            (5, "group-32 loop: 2 f16 MFMA + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2, 4)))
+            (5, "group-32 loop: 2 f16 MFMA + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2, 4)),
+            (6, "group-32 loop: i8 MFMA + cvt + fma, 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8,
+             ("random",), (2, 4)),
+            (7, "group-32 loop: 2 f16 MFMA + fma, 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8, ("random",),
+             (2, 4)))
     for kind, name, per_inst, peak, wpb, patterns, wps_list in plan:
         for pattern in patterns:
             c = codes[pattern]
             # int8: the bytes themselves; fp16: 8 codes per 16-byte fragment as fp16 values (exact)
-            src = (c[: 16 * 64 * 16].to(torch.int8) if kind not in (1, 5) else c[: 16 * 64 * 8].to(torch.float16)).to(dev)
+            src = (c[: 16 * 64 * 16].to(torch.int8) if kind not in (1, 5, 7) else c[: 16 * 64 * 8].to(torch.float16)).to(dev)
             for wps in wps_list:
                 blocks, iters = 256 * wps * 4 // wpb, 100000 // wps
                 call = lambda: lib.pq_probe_mfma(kind, ctypes.c_void_p(src.data_ptr()), blocks, iters,

@@ -15,6 +15,7 @@
 //           v_mfma_i32_32x32x32_i8 from zero, then acc = fma(scale, (float)partial, acc) on the 16 values per lane
 //   kind 5: the same group on fp16 MFMAs: two v_mfma_f32_32x32x16_f16 (the partial arrives in fp32, exact for
 //           int8 codes), then the 16 fmas; kinds 4 and 5 count 65536 int8-equivalent ops per group and tile
+//   kinds 6, 7: kinds 4, 5 in workgroups of 8 waves with waves 0-3 at issue priority 1, as kind 3
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -29,7 +30,7 @@ template <int KIND>
 __global__ __launch_bounds__(512) void mfma_ceiling_kernel(const v4i* __restrict__ src, int iters,
                                                            int* __restrict__ sink) {
   const int lane = threadIdx.x & 63;
-  if constexpr (KIND == 3) {
+  if constexpr (KIND == 3 || KIND == 6 || KIND == 7) {
     if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) < 4) __builtin_amdgcn_s_setprio(1);
   }
   v4i a[8], b[8];
@@ -38,7 +39,8 @@ __global__ __launch_bounds__(512) void mfma_ceiling_kernel(const v4i* __restrict
     a[i] = src[i * 64 + lane];
     b[i] = src[(8 + i) * 64 + lane];
   }
-  if constexpr (KIND == 4 || KIND == 5) {
+  if constexpr (KIND == 4 || KIND == 5 || KIND == 6 || KIND == 7) {
+    constexpr bool I8 = KIND == 4 || KIND == 6;
     // 2 x 2 tiles of fp32 accumulators; the group scales rotate through 8 registers per lane
     float sc[8];
 #pragma unroll
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(512) void mfma_ceiling_kernel(const v4i* __restrict
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const float sg = sc[(4 * g + t) & 7];
-          if constexpr (KIND == 4) {
+          if constexpr (I8) {
             const v16i part = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[2 * g + (t >> 1)], b[4 * g + (t & 1)], v16i{}, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[t][r] = __builtin_fmaf(sg, (float)part[r], acc[t][r]);
@@ -136,7 +138,7 @@ extern "C" int pq_probe_read(const void* src, int64_t bytes, int nt, int blocks,
   return (int)hipGetLastError();
 }
 
-// Runs the probe once: `blocks` workgroups of 4 waves (8 for kinds 2 and 3), `iters` x 8 MFMAs per wave, operands from `src` (16 x 64
+// Runs the probe once: `blocks` workgroups of 4 waves (8 for kinds 2, 3, 6 and 7), `iters` x 8 MFMAs per wave, operands from `src` (16 x 64
 // fragments of 16 bytes). Returns 0 or a HIP error code; the kernel time is left to the caller's events.
 extern "C" int pq_probe_mfma(int kind, const void* src, int blocks, int iters, int* sink, hipStream_t stream) {
   if (blocks < 1 || iters < 1 || !src || !sink) return -1;
@@ -157,6 +159,12 @@ extern "C" int pq_probe_mfma(int kind, const void* src, int blocks, int iters, i
                        iters, sink);
   } else if (kind == 5) {
     hipLaunchKernelGGL(mfma_ceiling_kernel<5>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
+                       iters, sink);
+  } else if (kind == 6) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel<6>, dim3(blocks), dim3(512), 0, stream, static_cast<const v4i*>(src),
+                       iters, sink);
+  } else if (kind == 7) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel<7>, dim3(blocks), dim3(512), 0, stream, static_cast<const v4i*>(src),
                        iters, sink);
   } else {
     return -1;
