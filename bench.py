@@ -50,6 +50,8 @@ def main() -> int:
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only run the register-only MFMA throughput probe (random / constant / zero operands, int8 "
                          "and fp16 MFMA) and print one JSON line")
+    ap.add_argument("--mfma-kinds", type=str, default=None,
+                    help="with --mfma-ceiling: comma-separated probe loops to run (0-11; default all)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the INT8 executor "
@@ -75,7 +77,8 @@ def main() -> int:
         print(json.dumps({"copy_probe_bytes": src.numel() * 4}), flush=True)
         return 0
     if args.mfma_ceiling:
-        print(json.dumps(mfma_ceiling(dev)), flush=True)
+        kinds = None if args.mfma_kinds is None else {int(k) for k in args.mfma_kinds.split(",")}
+        print(json.dumps(mfma_ceiling(dev, kinds)), flush=True)
         return 0
     if args.read_probe:
         print(json.dumps(read_probe(dev)), flush=True)
@@ -324,7 +327,7 @@ def read_probe(dev):
     return {"read_probe": cases}
 
 
-def mfma_ceiling(dev):
+def mfma_ceiling(dev, kinds=None):
     """Register-only MFMA loops (pyraquant_amd/csrc/probe/mfma_ceiling.hip) over the whole chip: the throughput the
     matrix cores sustain with no memory traffic at all, for random, constant and zero operands, at 1, 2 and 4 waves
     per SIMD. int8: v_mfma_i32_32x32x32_i8 against 5.0 POP/s; fp16: v_mfma_f32_32x32x16_f16 on the fp16 images of
@@ -359,12 +362,20 @@ def mfma_ceiling(dev):
             (6, "group-32 loop: i8 MFMA + cvt + fma, 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8,
              ("random",), (2, 4)),
             (7, "group-32 loop: 2 f16 MFMA + fma, 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8, ("random",),
-             (2, 4)))
+             (2, 4)),
+            (8, "group-32 loop, pipelined: 2 f16 MFMA + fma", 65536, INT8_PEAK_TOPS, 4, ("random", "constant"), (1, 2)),
+            (9, "group-32 loop, pipelined: i8 MFMA + cvt + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2)),
+            (10, "group-32 loop, pipelined: i8 MFMA from 1.5*2^23 + sub + fma", 65536, INT8_PEAK_TOPS, 4, ("random",),
+             (1, 2)),
+            (11, "group-32 loop, pipelined: i8 MFMA + fma only (timing reference)", 65536, INT8_PEAK_TOPS, 4,
+             ("random",), (1, 2)))
+    if kinds is not None:
+        plan = tuple(row for row in plan if row[0] in kinds)
     for kind, name, per_inst, peak, wpb, patterns, wps_list in plan:
         for pattern in patterns:
             c = codes[pattern]
             # int8: the bytes themselves; fp16: 8 codes per 16-byte fragment as fp16 values (exact)
-            src = (c[: 16 * 64 * 16].to(torch.int8) if kind not in (1, 5, 7) else c[: 16 * 64 * 8].to(torch.float16)).to(dev)
+            src = (c[: 16 * 64 * 16].to(torch.int8) if kind not in (1, 5, 7, 8) else c[: 16 * 64 * 8].to(torch.float16)).to(dev)
             for wps in wps_list:
                 blocks, iters = 256 * wps * 4 // wpb, 100000 // wps
                 call = lambda: lib.pq_probe_mfma(kind, ctypes.c_void_p(src.data_ptr()), blocks, iters,

@@ -16,8 +16,18 @@
 //   kind 5: the same group on fp16 MFMAs: two v_mfma_f32_32x32x16_f16 (the partial arrives in fp32, exact for
 //           int8 codes), then the 16 fmas; kinds 4 and 5 count 65536 int8-equivalent ops per group and tile
 //   kinds 6, 7: kinds 4, 5 in workgroups of 8 waves with waves 0-3 at issue priority 1, as kind 3
+//   kinds 8, 9: kinds 5, 4 software-pipelined: the partial of the tile two steps ahead is computed into its own
+//           register set while the fmas consume the current one, and fences fix the order (one MFMA, then a share
+//           of the fmas), so the wave's VALU work can run under its own MFMAs
+//   kind 10: kind 9 with the convert replaced by an exact float subtraction: the MFMA starts from the integer
+//           0x4B400000 (the bits of 1.5 * 2^23), so for a partial |p| < 2^22 the result reinterpreted as a float is
+//           1.5 * 2^23 + p exactly, and subtracting 1.5 * 2^23 gives (float)p bit for bit
+//   kind 11: kind 9 without the convert (the fma takes the partial's bits as a float): the fma-only cost, a timing
+//           reference whose sums mean nothing
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 namespace {
 
@@ -39,7 +49,78 @@ __global__ __launch_bounds__(512) void mfma_ceiling_kernel(const v4i* __restrict
     a[i] = src[i * 64 + lane];
     b[i] = src[(8 + i) * 64 + lane];
   }
-  if constexpr (KIND == 4 || KIND == 5 || KIND == 6 || KIND == 7) {
+  if constexpr (KIND >= 8) {
+    constexpr bool I8 = KIND != 8;
+    // kind 10: the partial's accumulator starts at the bits of 1.5 * 2^23 (see the kind list)
+    const v16i c0 = KIND == 10 ? v16i{} + 0x4B400000 : v16i{};
+    using part_t = typename std::conditional<I8, v16i, v16f>::type;
+    float sc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sc[i] = 1.0f + 1e-3f * (float)((lane + i) & 7);
+    v16f acc[4] = {v16f{}, v16f{}, v16f{}, v16f{}};
+    // Step j handles tile-group idx = j (idx = 4 g + t: K group g of 2, tile t of 2 x 2). Four partial buffers:
+    // step j issues the MFMA(s) of step j + 2 and runs the fmas of step j, whose partial was issued two steps
+    // earlier, so the fmas never wait on the MFMA in flight. Hard scheduling fences fix the order MFMA, half the
+    // fmas, [second fp16 MFMA, other half].
+    auto first = [&](int idx) -> part_t {
+      const int g = idx >> 2, t = idx & 3;
+      if constexpr (I8) return __builtin_amdgcn_mfma_i32_32x32x32_i8(a[2 * g + (t >> 1)], b[4 * g + (t & 1)], c0, 0, 0, 0);
+      else return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a[4 * g + (t >> 1)]),
+                                                         __builtin_bit_cast(v8h, b[4 * g + (t & 1)]), v16f{}, 0, 0, 0);
+    };
+    auto second = [&](int idx, part_t p) -> part_t {
+      const int g = idx >> 2, t = idx & 3;
+      if constexpr (I8) return p;
+      else return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a[4 * g + 2 + (t >> 1)]),
+                                                         __builtin_bit_cast(v8h, b[4 * g + 2 + (t & 1)]), p, 0, 0, 0);
+    };
+    part_t p[4];
+    p[0] = second(0, first(0));
+    p[1] = second(1, first(1));
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int idx = j, ahead = (j + 2) & 7;
+        const float sg = sc[idx];
+        v16f& ac = acc[idx & 3];
+        part_t& cur = p[j & 3];
+        part_t& nxt = p[(j + 2) & 3];
+        nxt = first(ahead);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (KIND == 10) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) ac[r] = __builtin_fmaf(sg, __int_as_float(cur[r]) - 12582912.0f, ac[r]);
+          __builtin_amdgcn_sched_barrier(0);
+        } else if constexpr (KIND == 11) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) ac[r] = __builtin_fmaf(sg, __int_as_float(cur[r]), ac[r]);
+          __builtin_amdgcn_sched_barrier(0);
+        } else if constexpr (I8) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) ac[r] = __builtin_fmaf(sg, (float)cur[r], ac[r]);
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 8; ++r) ac[r] = __builtin_fmaf(sg, cur[r], ac[r]);
+          __builtin_amdgcn_sched_barrier(0);
+          nxt = second(ahead, nxt);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int r = 8; r < 16; ++r) ac[r] = __builtin_fmaf(sg, cur[r], ac[r]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    part_t cur = p[0] + p[1];
+    float s = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += (float)cur[r];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s += acc[j][r];
+    sink[blockIdx.x * blockDim.x + threadIdx.x] = __float_as_int(s);
+  } else if constexpr (KIND == 4 || KIND == 5 || KIND == 6 || KIND == 7) {
     constexpr bool I8 = KIND == 4 || KIND == 6;
     // 2 x 2 tiles of fp32 accumulators; the group scales rotate through 8 registers per lane
     float sc[8];
@@ -165,6 +246,18 @@ extern "C" int pq_probe_mfma(int kind, const void* src, int blocks, int iters, i
                        iters, sink);
   } else if (kind == 7) {
     hipLaunchKernelGGL(mfma_ceiling_kernel<7>, dim3(blocks), dim3(512), 0, stream, static_cast<const v4i*>(src),
+                       iters, sink);
+  } else if (kind == 8) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel<8>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
+                       iters, sink);
+  } else if (kind == 9) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel<9>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
+                       iters, sink);
+  } else if (kind == 10) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel<10>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
+                       iters, sink);
+  } else if (kind == 11) {
+    hipLaunchKernelGGL(mfma_ceiling_kernel<11>, dim3(blocks), dim3(256), 0, stream, static_cast<const v4i*>(src),
                        iters, sink);
   } else {
     return -1;
