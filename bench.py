@@ -109,7 +109,7 @@ def main() -> int:
         fused = q.weight_packed is not None and q.lr_At is not None
         if fused:   # quantizer + low-rank down-projection in one pass over x, as Int8Linear.forward runs it
             e1 = e0
-            xq, sx, t = E.quant_rows_lowrank(x, q.lr_At, rows)
+            xq, sx, t = E.quant_rows_lowrank(x, q.lr_At, rows, q._lr_frag())
             e2 = mark()
         else:
             t = E.lowrank_down(x, q.lr_At, rows) if q.lr_At is not None else None

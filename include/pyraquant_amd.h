@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define PQ_ABI_VERSION 1
+#define PQ_ABI_VERSION 2
 
 /* status codes */
 #define PQ_OK 0
@@ -148,10 +148,22 @@ int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
  * accumulation order differs, so the last bit of t may differ from it). x is read from HBM once when R == 32,
  * K is one of 1024, 1280, 2048, 2560, 3072, rows are 16-byte aligned (ldx % 8 == 0) and every x byte offset fits
  * 30 bits; other shapes run the two kernels. l1t [R, K] contiguous, same dtype as x; t [M, R] with row stride ldt.
+ * l1f: NULL, or the same matrix in the one-pass kernel's fragment order (pq_pack_lowrank_l1t, 16-byte aligned),
+ * which that kernel then reads instead of l1t (contiguous 1 KB register loads: 15.1 -> 12.7 us at M = 4096,
+ * K = 3072); results are identical either way, and l1t is still required (the other paths read it).
  */
 int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
-                          const int32_t* row_idx, const void* l1t, int64_t R, int8_t* qp, float* s, void* t,
-                          int64_t ldt, hipStream_t stream);
+                          const int32_t* row_idx, const void* l1t, const void* l1f, int64_t R, int8_t* qp, float* s,
+                          void* t, int64_t ldt, hipStream_t stream);
+
+/*
+ * Write l1t [R, K] (bf16/fp16, contiguous, 16-byte aligned) in the fragment order pq_quant_rows_lowrank's one-pass
+ * kernel loads from its l1f argument: l1f receives R * K 16-bit values (16-byte aligned). Defined for R == 32 and
+ * K in {1024, 1280, 2048, 2560, 3072} (the one-pass shapes); PQ_ESHAPE otherwise, and callers then pass l1f = NULL.
+ * One-off at weight conversion, like pq_pack_k64. No reference counterpart (the reference multiplies by lr_A
+ * [K, R] with torch, deploy/int8_exec.py:390).
+ */
+int pq_pack_lowrank_l1t(const void* l1t, int32_t dtype, int64_t R, int64_t K, void* l1f, hipStream_t stream);
 
 /*
  * Fused INT8 GEMM over packed K64 operands (ap: activation codes [M, K], wp: weights [N, K], both in the packed
@@ -185,12 +197,13 @@ int64_t pq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t R);
  * in use until the GEMM has run on `stream`). x [M, K] bf16/fp16 (row stride ldx); w_packed the packed K64
  * weights [N, K]; s_w [N] (group 0) or [K/32, N] (group 32); bias [N] fp32 or NULL; l1t [R, K] and l2t [N, Re] in
  * x's dtype (R a multiple of 32 up to 128, Re in {16, 32, 64} and Re <= R: the first Re columns of t enter the
- * epilogue), or NULL with R = Re = 0; y [M, N] in x's dtype with row stride ldy. Same results as the two calls.
+ * epilogue), or NULL with R = Re = 0; l1f NULL or l1t in fragment order (as pq_quant_rows_lowrank); y [M, N] in
+ * x's dtype with row stride ldy. Same results as the two calls.
  * Replaces the body of `Int8Linear.forward` (deploy/int8_exec.py:382-393): one C call per layer.
  */
 int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
-                   const float* s_w, int64_t group, const float* bias, const void* l1t, int64_t R, const void* l2t,
-                   int64_t Re, void* y, int64_t ldy, int64_t N, void* workspace, int64_t ws_bytes,
+                   const float* s_w, int64_t group, const float* bias, const void* l1t, const void* l1f, int64_t R,
+                   const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N, void* workspace, int64_t ws_bytes,
                    hipStream_t stream);
 
 /*
@@ -205,8 +218,9 @@ int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t
  * pq_int8_linear.
  */
 int pq_int8_linear_noalloc(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
-                           const float* s_w, int64_t group, const float* bias, const void* l1t, int64_t R,
-                           const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N, hipStream_t stream);
+                           const float* s_w, int64_t group, const float* bias, const void* l1t, const void* l1f,
+                           int64_t R, const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N,
+                           hipStream_t stream);
 
 /* Bytes of the device array behind pq_int8_linear_noalloc (its largest staging). No reference counterpart. */
 int64_t pq_int8_linear_noalloc_max_bytes(void);

@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpqint8.s
 PQ_OK, PQ_EINVAL, PQ_ESHAPE, PQ_EALIGN, PQ_EDTYPE, PQ_ELAUNCH = 0, -1, -2, -3, -4, -5
 PQ_BF16, PQ_F16, PQ_I32 = 0, 1, 2
 PQ_ACCUMULATE = 0x100   # OR'ed into pq_int8_gemm_packed's out_dtype
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # every entry point declared in include/pyraquant_amd.h
 EXPORTS = (
@@ -32,6 +32,7 @@ EXPORTS = (
     "pq_pack_k64",
     "pq_quant_rows_packed",
     "pq_quant_rows_lowrank",
+    "pq_pack_lowrank_l1t",
     "pq_dequant_epilogue",
     "pq_route_union_rows",
     "pq_route_patches",
@@ -62,7 +63,8 @@ _SIGNATURES = {
                             ctypes.c_int),
     "pq_pack_k64": ([_p, _i64, _i64, _i64, _p, _p], ctypes.c_int),
     "pq_quant_rows_packed": ([_p, _i32, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
-    "pq_quant_rows_lowrank": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p], ctypes.c_int),
+    "pq_quant_rows_lowrank": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _p, _p, _i64, _p], ctypes.c_int),
+    "pq_pack_lowrank_l1t": ([_p, _i32, _i64, _i64, _p, _p], ctypes.c_int),
     "pq_dequant_epilogue": ([_p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p], ctypes.c_int),
     "pq_route_union_rows": ([_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "pq_route_patches": ([_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p], ctypes.c_int),
@@ -71,10 +73,10 @@ _SIGNATURES = {
                         ctypes.c_int),
     "pq_fold_weight": ([_p, _i32, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p, _i64, _p, _p], ctypes.c_int),
     "pq_int8_linear_workspace_size": ([_i64, _i64, _i64], _i64),
-    "pq_int8_linear": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p],
-                       ctypes.c_int),
-    "pq_int8_linear_noalloc": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p],
-                               ctypes.c_int),
+    "pq_int8_linear": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _i64,
+                        _p], ctypes.c_int),
+    "pq_int8_linear_noalloc": ([_p, _i32, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64,
+                                _p], ctypes.c_int),
     "pq_int8_linear_noalloc_max_bytes": ([], _i64),
 }
 

@@ -32,14 +32,14 @@ LayerSlices layer_slices(int64_t M, int64_t K, int64_t R) {
 }  // namespace
 
 // The layer over a workspace the caller provides (shared by pq_int8_linear and its allocation-free variant).
-int run_layer(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
-              const float* s_w, int64_t group, const float* bias, const void* l1t, int64_t R, const void* l2t,
-              int64_t Re, void* y, int64_t ldy, int64_t N, uint8_t* ws, hipStream_t stream) {
+static int run_layer(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
+                     const float* s_w, int64_t group, const float* bias, const void* l1t, const void* l1f, int64_t R,
+                     const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N, uint8_t* ws, hipStream_t stream) {
   const LayerSlices sl = layer_slices(M, K, R);
   int8_t* const q = reinterpret_cast<int8_t*>(ws);
   float* const s = reinterpret_cast<float*>(ws + sl.scales);
   void* const t = R ? static_cast<void*>(ws + sl.t) : nullptr;
-  int st = R ? pq_quant_rows_lowrank(x, x_dtype, M, K, ldx, M, nullptr, l1t, R, q, s, t, R, stream)
+  int st = R ? pq_quant_rows_lowrank(x, x_dtype, M, K, ldx, M, nullptr, l1t, l1f, R, q, s, t, R, stream)
              : pq_quant_rows_packed(x, x_dtype, M, K, ldx, nullptr, q, s, stream);
   if (st != PQ_OK) return st;
   return pq_int8_gemm_packed(q, w_packed, s, s_w, group, bias, R ? t : nullptr, R, R ? l2t : nullptr, Re, x_dtype, y,
@@ -68,7 +68,8 @@ extern "C" int64_t pq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t R
 
 extern "C" int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
                               const int8_t* w_packed, const float* s_w, int64_t group, const float* bias,
-                              const void* l1t, int64_t R, const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N,
+                              const void* l1t, const void* l1f, int64_t R, const void* l2t, int64_t Re, void* y,
+                              int64_t ldy, int64_t N,
                               void* workspace, int64_t ws_bytes, hipStream_t stream) {
   int st = check_layer(M, K, N, R, Re, l1t, l2t, "pq_int8_linear");
   if (st != PQ_OK || M == 0) return st;
@@ -77,7 +78,7 @@ extern "C" int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t
     return set_error(PQ_ESHAPE, "pq_int8_linear: the workspace holds %lld bytes, the layer needs %lld", (long long)ws_bytes,
                      (long long)need);
   if ((uintptr_t)workspace % 256) return set_error(PQ_EALIGN, "pq_int8_linear: the workspace must be 256-byte aligned");
-  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, R, l2t, Re, y, ldy, N,
+  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, l1f, R, l2t, Re, y, ldy, N,
                    static_cast<uint8_t*>(workspace), stream);
 }
 
@@ -127,7 +128,8 @@ extern "C" int64_t pq_int8_linear_noalloc_max_bytes(void) { return kScratchBytes
 
 extern "C" int pq_int8_linear_noalloc(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
                                       const int8_t* w_packed, const float* s_w, int64_t group, const float* bias,
-                                      const void* l1t, int64_t R, const void* l2t, int64_t Re, void* y, int64_t ldy,
+                                      const void* l1t, const void* l1f, int64_t R, const void* l2t, int64_t Re,
+                                      void* y, int64_t ldy,
                                       int64_t N, hipStream_t stream) {
   int st = check_layer(M, K, N, R, Re, l1t, l2t, "pq_int8_linear_noalloc");
   if (st != PQ_OK || M == 0) return st;
@@ -140,5 +142,5 @@ extern "C" int pq_int8_linear_noalloc(const void* x, int32_t x_dtype, int64_t M,
   uint8_t* ws = nullptr;
   st = device_scratch(stream, &ws);
   if (st != PQ_OK) return st;
-  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, R, l2t, Re, y, ldy, N, ws, stream);
+  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, l1f, R, l2t, Re, y, ldy, N, ws, stream);
 }

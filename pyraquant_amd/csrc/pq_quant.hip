@@ -409,6 +409,10 @@ __device__ __forceinline__ int row_byte_offset(int64_t m, int64_t M, const int32
 //   registers (quant_chunk), each wave storing whole 16-row x 64-byte packed K64 blocks;
 //   t partial = the slice of x . l1t by v_mfma_f32_16x16x32, whose l1t slice stays in registers for the whole
 //   kernel -> LDS -> t = (..((p0 + p1) + p2) ..) + p(W-1) in fp32, rounded to the 16-bit type.
+// The l1t slice comes from l1f when given: the same matrix in fragment order (pack_lowrank_l1t_kernel), where each
+// of the wave's 4 NC register loads is one contiguous 1 KB piece. From row-major l1t each load touches 16 rows at
+// half a cache line apiece; with one batch per workgroup (c0: M = 4096, 256 batches) the whole 192 KB slice set is
+// on the critical path, and the fragment order takes the pass from 15.1 to 12.7 us.
 // W = 16 where K allows it (K % 1024 == 0), else 8, else 4: the batch's work is spread over more waves while the
 // single LDS batch buffer (the memory pipeline) stays the same (c1: 143 -> 130 us from W = 4 to 16).
 // K assignment inside the 64-wide K block c of a slice (MFMA steps 2c and 2c + 1): lane group g covers
@@ -417,8 +421,8 @@ __device__ __forceinline__ int row_byte_offset(int64_t m, int64_t M, const int32
 template <int DT, int NC, int W>   // W waves, NC: 64-wide K blocks per wave, K = 64 W NC
 __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int64_t M, const int32_t* __restrict__ row_idx,
-    const uint16_t* __restrict__ l1t, int8_t* __restrict__ qp, float* __restrict__ s, uint16_t* __restrict__ t,
-    int64_t ldt, int nbatch) {
+    const uint16_t* __restrict__ l1t, const uint16_t* __restrict__ l1f, int8_t* __restrict__ qp,
+    float* __restrict__ s, uint16_t* __restrict__ t, int64_t ldt, int nbatch) {
   constexpr int K = 64 * W * NC, R = 32, NS = 2 * NC;
   constexpr int CHUNKS = (2 * K + 1023) / 1024;      // 1 KB DMA pieces per row
   constexpr int PITCH = CHUNKS * 1024 + 64;          // LDS row pitch (+64 bytes: rows start 16 banks apart)
@@ -465,13 +469,22 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
   // instead of queueing behind them (at small M every workgroup runs a single batch, so nothing else hides it).
   __builtin_amdgcn_sched_barrier(0);
   // l1t fragments of this wave's slice: lf[h][2 c + e] = l1t[16 h + r][k0 + 64 c + 16 g + 8 e .. + 8]
+  // (in l1f: 16-byte piece ((wave * 2 + h) * NS + 2 c + e) * 64 + lane)
   v4u lf[2][NS];
+  if (l1f) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int i = 0; i < NS; ++i)
-      lf[h][i] = *reinterpret_cast<const v4u*>(l1t + (int64_t)(16 * h + r) * K + k0 + 64 * (i >> 1) + 16 * g +
-                                               8 * (i & 1));
+      for (int i = 0; i < NS; ++i)
+        lf[h][i] = *reinterpret_cast<const v4u*>(l1f + ((int64_t)((wave * 2 + h) * NS + i) * 64 + lane) * 8);
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < NS; ++i)
+        lf[h][i] = *reinterpret_cast<const v4u*>(l1t + (int64_t)(16 * h + r) * K + k0 + 64 * (i >> 1) + 16 * g +
+                                                 8 * (i & 1));
+  }
   // One batch. The first batch's DMA is followed only by the l1t loads (4 NC of them), which may stay in flight: the
   // low-rank MFMAs that need them come after the codes, so the l1t reads land under that work (at small M every
   // workgroup runs one batch and nothing else would hide them). The first batch is peeled off the loop, so that the
@@ -561,6 +574,31 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
   };
   if (b < nbatch) batch(b, std::true_type{});
   for (b += G; b < nbatch; b += G) batch(b, std::false_type{});
+}
+
+// Waves per workgroup of quant_lowrank_kernel for rank R and row length K, or 0 where it does not apply: R == 32
+// and K / 256 in {4, 5, 8, 10, 12}; W = 16 when K % 1024 == 0, 8 when K % 512 == 0, else 4.
+inline int lowrank_fused_waves(int64_t R, int64_t K) {
+  if (R != 32 || K % 256 != 0) return 0;
+  const int64_t nc = K / 256;
+  if (nc != 4 && nc != 5 && nc != 8 && nc != 10 && nc != 12) return 0;
+  return nc % 4 == 0 ? 16 : nc % 2 == 0 ? 8 : 4;
+}
+
+// l1t [32, K] -> the fragment order quant_lowrank_kernel loads from l1f (W waves, NS = K / (32 W) loads of 16 bytes
+// per lane and half): piece p = ((w * 2 + h) * NS + i) * 64 + l holds l1t[16 h + l % 16][w K / W + 64 (i / 2) +
+// 16 (l / 16) + 8 (i % 2) .. + 8]. One thread per 16-byte piece (4 K of them).
+__global__ __launch_bounds__(256) void pack_lowrank_l1t_kernel(const v4u* __restrict__ src, int K, int W,
+                                                               v4u* __restrict__ dst) {
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= 4 * K) return;
+  const int NS = K / (32 * W);
+  const int l = p & 63, rest = p >> 6;
+  const int i = rest % NS, wh = rest / NS;
+  const int h = wh & 1, w = wh >> 1;
+  const int row = 16 * h + (l & 15);
+  const int col = w * (K / W) + 64 * (i >> 1) + 16 * (l >> 4) + 8 * (i & 1);
+  dst[p] = src[(row * K + col) / 8];
 }
 
 // ---- fused quantizer + low-rank down-projection for wide rows (K = 4096 .. 12288) ---------------------------------
@@ -866,14 +904,14 @@ extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t 
 // pq_quant_rows_packed and pq_lowrank_down on the same x, with x read once where the fused kernel applies
 // (R == 32, K in {1024, 1280, 2048, 2560, 3072}, 16-byte aligned rows, 32-bit x offsets); otherwise the two.
 extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
-                                     int64_t x_rows, const int32_t* row_idx, const void* l1t, int64_t R, int8_t* qp,
-                                     float* s, void* t, int64_t ldt, hipStream_t stream) {
+                                     int64_t x_rows, const int32_t* row_idx, const void* l1t, const void* l1f,
+                                     int64_t R, int8_t* qp, float* s, void* t, int64_t ldt, hipStream_t stream) {
   if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_rows_lowrank: bad shape M=%lld K=%lld", (long long)M, (long long)K);
   if (M == 0) return PQ_OK;
   if (!x || !qp || !s || !l1t || !t) return set_error(PQ_EINVAL, "pq_quant_rows_lowrank: null pointer");
+  if (l1f && (uintptr_t)l1f % 16) return set_error(PQ_EINVAL, "pq_quant_rows_lowrank: l1f must be 16-byte aligned");
   const int nc = (int)(K / 256);
-  const bool fused = R == 32 && K % 256 == 0 && (nc == 4 || nc == 5 || nc == 8 || nc == 10 || nc == 12) &&
-                     ldx >= K && ldx % 8 == 0 && ldt >= R && ldt % 2 == 0 && x_rows >= 1 &&
+  const bool fused = lowrank_fused_waves(R, K) != 0 && ldx >= K && ldx % 8 == 0 && ldt >= R && ldt % 2 == 0 && x_rows >= 1 &&
                      (row_idx || x_rows >= M) && x_rows * ldx * 2 + 2 * K <= 0x3fffffffLL &&
                      (uintptr_t)x % 16 == 0 && (uintptr_t)l1t % 16 == 0 && (uintptr_t)t % 4 == 0 &&
                      (uintptr_t)qp % 16 == 0 && (x_dtype == PQ_BF16 || x_dtype == PQ_F16);
@@ -907,12 +945,13 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
   const dim3 grid((unsigned)std::min(nbatch, 256));
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* lp = static_cast<const uint16_t*>(l1t);
+  const uint16_t* fp = static_cast<const uint16_t*>(l1f);
   uint16_t* tp = static_cast<uint16_t*>(t);
-  // nc = K / 256; W = 16 waves when nc % 4 == 0, 8 when nc % 2 == 0, else 4
+  // nc = K / 256; W = 16 waves when nc % 4 == 0, 8 when nc % 2 == 0, else 4 (lowrank_fused_waves)
 #define PQ_QLCASE(D, NC, W)                                                                                  \
   if (x_dtype == D && nc == NC) {                                                                           \
     hipLaunchKernelGGL((quant_lowrank_kernel<D, NC * 4 / W, W>), grid, dim3(64 * W), 0, stream, xp, ldx, x_rows, \
-                       M, row_idx, lp, qp, s, tp, ldt, nbatch);                                             \
+                       M, row_idx, lp, fp, qp, s, tp, ldt, nbatch);                                         \
     return check_launch("quant_rows_lowrank");                                                              \
   }
   PQ_QLCASE(PQ_BF16, 4, 16) PQ_QLCASE(PQ_BF16, 5, 4) PQ_QLCASE(PQ_BF16, 8, 16) PQ_QLCASE(PQ_BF16, 10, 8)
@@ -921,6 +960,19 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
   PQ_QLCASE(PQ_F16, 12, 16)
 #undef PQ_QLCASE
   return set_error(PQ_ESHAPE, "pq_quant_rows_lowrank: unsupported shape");
+}
+
+extern "C" int pq_pack_lowrank_l1t(const void* l1t, int32_t dtype, int64_t R, int64_t K, void* l1f, hipStream_t stream) {
+  if (!l1t || !l1f) return set_error(PQ_EINVAL, "pq_pack_lowrank_l1t: null pointer");
+  if (dtype != PQ_BF16 && dtype != PQ_F16) return set_error(PQ_EDTYPE, "pq_pack_lowrank_l1t: dtype must be bf16 or fp16");
+  const int W = lowrank_fused_waves(R, K);
+  if (W == 0)
+    return set_error(PQ_ESHAPE, "pq_pack_lowrank_l1t: the fragment order exists for R == 32 and K in {1024, 1280, "
+                                "2048, 2560, 3072} only (got R=%lld K=%lld)", (long long)R, (long long)K);
+  if ((uintptr_t)l1t % 16 || (uintptr_t)l1f % 16) return set_error(PQ_EINVAL, "pq_pack_lowrank_l1t: 16-byte alignment");
+  hipLaunchKernelGGL(pack_lowrank_l1t_kernel, dim3((unsigned)((4 * K + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const v4u*>(l1t), (int)K, W, static_cast<v4u*>(l1f));
+  return check_launch("pack_lowrank_l1t");
 }
 
 extern "C" int pq_dequant_epilogue(const int32_t* acc, const float* s_row, const float* s_col,

@@ -243,10 +243,31 @@ def quant_rows_packed(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) 
     return q, s
 
 
-def quant_rows_lowrank(x2: torch.Tensor, lr_At: torch.Tensor,
-                       row_idx: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+def lowrank_l1t_packable(R: int, K: int) -> bool:
+    """Whether pq_pack_lowrank_l1t defines a fragment order for lr_At [R, K] (the one-pass quantizer's shapes)."""
+    return R == 32 and K % 256 == 0 and K // 256 in (4, 5, 8, 10, 12)
+
+
+def pack_lowrank_l1t(lr_At: torch.Tensor) -> Optional[torch.Tensor]:
+    """lr_At [R, K] in the one-pass quantizer's fragment order (pq_pack_lowrank_l1t), a tensor of the same shape and
+    dtype whose memory the kernel reads as contiguous 1 KB register loads; None where no such order exists. Int8Linear
+    packs it once at conversion, beside lr_At."""
+    assert lr_At.dim() == 2 and lr_At.is_cuda and lr_At.is_contiguous()
+    R, K = lr_At.shape
+    if not lowrank_l1t_packable(R, K) or lr_At.dtype not in (torch.bfloat16, torch.float16):
+        return None
+    out = torch.empty_like(lr_At)
+    L = _lib.load()
+    _lib.check(L.pq_pack_lowrank_l1t(_lib.ptr(lr_At), _lib.dtype_code(lr_At.dtype), R, K, _lib.ptr(out),
+                                     _lib.stream_of(lr_At.device)), "pack_lowrank_l1t")
+    return out
+
+
+def quant_rows_lowrank(x2: torch.Tensor, lr_At: torch.Tensor, row_idx: Optional[torch.Tensor] = None,
+                       lr_At_frag: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """quant_rows_packed(x2, row_idx) and lowrank_down(x2, lr_At, row_idx) from one pass over x2
-    (pq_quant_rows_lowrank; deploy/int8_exec.py:390-391). Returns (packed codes, scales, t)."""
+    (pq_quant_rows_lowrank; deploy/int8_exec.py:390-391). Returns (packed codes, scales, t). ``lr_At_frag``: lr_At in
+    fragment order (pack_lowrank_l1t) or None; the results are the same either way."""
     assert x2.dim() == 2 and x2.is_cuda and lr_At.is_cuda
     if x2.stride(1) != 1:
         x2 = x2.contiguous()
@@ -255,6 +276,9 @@ def quant_rows_lowrank(x2: torch.Tensor, lr_At: torch.Tensor,
     assert K % 64 == 0, K
     assert lr_At.is_contiguous() and lr_At.shape[1] == K, "lr_At must be [R, K] contiguous"
     R = lr_At.shape[0]
+    if lr_At_frag is not None:
+        assert lr_At_frag.shape == lr_At.shape and lr_At_frag.dtype == lr_At.dtype and lr_At_frag.is_contiguous()
+        assert lr_At_frag.device == lr_At.device
     ri = _row_index(row_idx, x2.device)
     M = rows if ri is None else ri.shape[0]
     q = torch.empty((packed_rows(M) * K,), dtype=torch.int8, device=x2.device)
@@ -262,8 +286,8 @@ def quant_rows_lowrank(x2: torch.Tensor, lr_At: torch.Tensor,
     t = torch.empty((M, R), dtype=x2.dtype, device=x2.device)
     L = _lib.load()
     _lib.check(L.pq_quant_rows_lowrank(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), rows, _lib.ptr(ri),
-                                       _lib.ptr(lr_At), R, _lib.ptr(q), _lib.ptr(s), _lib.ptr(t), R,
-                                       _lib.stream_of(x2.device)), "quant_rows_lowrank")
+                                       _lib.ptr(lr_At), _lib.ptr(lr_At_frag), R, _lib.ptr(q), _lib.ptr(s),
+                                       _lib.ptr(t), R, _lib.stream_of(x2.device)), "quant_rows_lowrank")
     return q, s, t
 
 
@@ -372,7 +396,8 @@ class Int8Linear(nn.Module):
 
     Buffers as in the reference: ``weight_int8`` [N, K], ``w_scale`` ([N]; [N, K/32] with group_size=32),
     ``bias`` (fp32) and ``lr_A`` [K, R] / ``lr_B`` [R, N]. Kernel-layout copies: ``lr_At`` [R, K], ``lr_Bt``
-    [N, R] and, for group_size=32, ``w_scale_gn`` [K/32, N]."""
+    [N, R], ``lr_At_frag`` (lr_At in the one-pass quantizer's fragment order where one exists, else None; not saved
+    in the state dict) and, for group_size=32, ``w_scale_gn`` [K/32, N]."""
 
     def __init__(self, lin: nn.Linear, device: Optional[torch.device] = None,
                  lowrank: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, group_size: int = 0):
@@ -421,6 +446,7 @@ class Int8Linear(nn.Module):
                 At = A.new_zeros((r_down, K))
                 At[:R] = A.t()
             self.register_buffer("lr_At", At)
+            self.register_buffer("lr_At_frag", None if At is None else pack_lowrank_l1t(At), persistent=False)
             Bt = B.new_zeros((N, r_epi)) if r_epi else None
             if Bt is not None:
                 Bt[:, :R] = B.t()
@@ -429,6 +455,7 @@ class Int8Linear(nn.Module):
             self.lr_A = None
             self.lr_B = None
             self.lr_At = None
+            self.lr_At_frag = None
             self.lr_Bt = None
         del w
 
@@ -446,6 +473,13 @@ class Int8Linear(nn.Module):
             if new is not None and new.dtype != torch.float32:
                 self._buffers[n] = old.to(new.device)
         return self
+
+    def _lr_frag(self) -> Optional[torch.Tensor]:
+        """lr_At_frag where it still matches lr_At (a module-wide cast or move carries both the same way)."""
+        f = self.lr_At_frag
+        if f is None or self.lr_At is None or f.dtype != self.lr_At.dtype or f.device != self.lr_At.device:
+            return None
+        return f
 
     def _scale_k(self) -> torch.Tensor:
         return self.w_scale_gn if self.group_size else self.w_scale
@@ -477,6 +511,7 @@ class Int8Linear(nn.Module):
         Re = 0 if self.lr_Bt is None else self.lr_Bt.shape[1]         # rank of the epilogue
         if R and (self.lr_At.dtype != dt or self.lr_Bt.dtype != dt):
             return None
+        frag = self._lr_frag()
         # the GEMM reads these as fp32 through raw pointers: anything else goes to the general path, which asserts
         sk = self._scale_k()
         if sk.dtype != torch.float32 or sk.device != x.device or not sk.is_contiguous():
@@ -490,7 +525,8 @@ class Int8Linear(nn.Module):
         out = torch.empty((M, N), dtype=dt, device=dev)
         st = L.pq_int8_linear(x2.data_ptr(), code, M, K, x2.stride(0), self.weight_packed.data_ptr(), sk.data_ptr(),
                               self.group_size, None if self.bias is None else self.bias.data_ptr(),
-                              self.lr_At.data_ptr() if R else None, R, self.lr_Bt.data_ptr() if R else None, Re,
+                              self.lr_At.data_ptr() if R else None, frag.data_ptr() if R and frag is not None else None,
+                              R, self.lr_Bt.data_ptr() if R else None, Re,
                               out.data_ptr(), N, N, ws.data_ptr(), ws.numel(), _raw_stream(dev))
         if st:
             _lib.check(st, "int8_linear")
@@ -518,7 +554,7 @@ class Int8Linear(nn.Module):
         fused = self.weight_packed is not None and self.lr_At is not None and x2.dtype == self.lr_A.dtype
         if fused:
             # quantizer and low-rank down-projection from one pass over x (deploy/int8_exec.py:390-391)
-            xq, sx, t = quant_rows_lowrank(x2, self.lr_At, row_idx)
+            xq, sx, t = quant_rows_lowrank(x2, self.lr_At, row_idx, self._lr_frag())
         elif self.lr_A is not None:
             xl = x2 if x2.dtype == self.lr_A.dtype else x2.to(self.lr_A.dtype)
             if self.lr_At is not None:

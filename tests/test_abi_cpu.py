@@ -179,3 +179,24 @@ def test_lowrank_widths():
               65: (96, 0), 96: (96, 0), 128: (128, 0), 129: (0, 0), 200: (0, 0)}
     for r, w in expect.items():
         assert _lowrank_widths(r) == w, (r, _lowrank_widths(r), w)
+
+
+def test_pack_lowrank_l1t_rejects_without_gpu(lib):
+    """pq_pack_lowrank_l1t refuses shapes without a fragment order, bad dtypes and null or misaligned pointers before
+    any HIP call; pq_quant_rows_lowrank refuses a misaligned l1f the same way. lowrank_l1t_packable states the same
+    shape rule on the host."""
+    import pyraquant_amd._lib as L
+    from pyraquant_amd.int8_exec import lowrank_l1t_packable
+
+    p16, nul = ctypes.c_void_p(256), None
+    assert lib.pq_pack_lowrank_l1t(nul, 0, 32, 3072, p16, nul) == L.PQ_EINVAL
+    assert lib.pq_pack_lowrank_l1t(p16, 2, 32, 3072, p16, nul) == L.PQ_EDTYPE
+    for R, K in ((64, 3072), (16, 3072), (32, 4096), (32, 3136), (32, 768), (32, 12288)):
+        assert not lowrank_l1t_packable(R, K)
+        assert lib.pq_pack_lowrank_l1t(p16, 0, R, K, p16, nul) == L.PQ_ESHAPE, (R, K)
+    assert b"fragment order" in lib.pq_last_error()
+    assert lib.pq_pack_lowrank_l1t(p16, 1, 32, 1280, ctypes.c_void_p(264), nul) == L.PQ_EINVAL
+    assert [K for K in range(256, 16384, 256) if lowrank_l1t_packable(32, K)] == [1024, 1280, 2048, 2560, 3072]
+    assert lib.pq_quant_rows_lowrank(p16, 0, 16, 3072, 3072, 16, nul, p16, ctypes.c_void_p(264), 32, p16, p16, p16, 32,
+                                     nul) == L.PQ_EINVAL
+    assert b"l1f" in lib.pq_last_error()

@@ -44,7 +44,7 @@ def _packed_rows(qp: torch.Tensor, rows: torch.Tensor, K: int) -> np.ndarray:
 def _first_stage(E, q, x2, row_idx=None):
     """The codes, scales (and t) of the layer's first kernel, through the entry point Int8Linear.forward uses."""
     if q.lr_At is not None:
-        return E.quant_rows_lowrank(x2, q.lr_At, row_idx)
+        return E.quant_rows_lowrank(x2, q.lr_At, row_idx, q._lr_frag())
     xq, sx = E.quant_rows_packed(x2, row_idx)
     return xq, sx, None
 

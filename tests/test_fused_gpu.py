@@ -5,7 +5,9 @@
 * t within bf16 rounding of the float64 product and within the build's tolerance of the oracle's fp32 result;
 * K = 4096 .. 12288 in steps of 2048 (c2a's 12288) run the wide kernel, which holds rows in registers: the same bar;
 * other shapes (K outside both lists, R != 32) run the two kernels: the same bar, and exactly what the two separate
-  entry points give.
+  entry points give;
+* the fragment-order copy of l1t (pq_pack_lowrank_l1t) matches its documented index formula, and the one-pass kernel
+  gives the same bits from it as from l1t.
 """
 import numpy as np
 import pytest
@@ -126,3 +128,80 @@ def test_int8linear_uses_fused_pass(oracle, cuda):
                       bits(q.lr_A), bits(q.lr_B))
     mx, mean = rel_errors(oracle.to_f32(bits(y), 0), o["y"])
     assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
+def _fragment_order_np(l1t: np.ndarray) -> np.ndarray:
+    """The fragment order pq_pack_lowrank_l1t documents, from its index formula (numpy, uint16 bits): piece
+    p = ((w * 2 + h) * NS + i) * 64 + l of 8 values holds l1t[16 h + l % 16][w K / W + 64 (i // 2) + 16 (l // 16)
+    + 8 (i % 2) + (0..7)], W = 16 / 8 / 4 waves for K / 256 divisible by 4 / 2 / neither, NS = K / (32 W)."""
+    R, K = l1t.shape
+    nc = K // 256
+    W = 16 if nc % 4 == 0 else (8 if nc % 2 == 0 else 4)
+    NS = K // (32 * W)
+    out = np.empty((4 * K, 8), dtype=l1t.dtype)
+    for p in range(4 * K):
+        l, rest = p % 64, p // 64
+        i, wh = rest % NS, rest // NS
+        h, w = wh % 2, wh // 2
+        col = w * (K // W) + 64 * (i // 2) + 16 * (l // 16) + 8 * (i % 2)
+        out[p] = l1t[16 * h + l % 16, col:col + 8]
+    return out.reshape(R, K)
+
+
+@pytest.mark.parametrize("K", [1024, 1280, 2048, 2560, 3072])
+def test_pack_lowrank_l1t_order(cuda, K):
+    """pq_pack_lowrank_l1t against its documented index formula, bit for bit; a permutation (every value once)."""
+    from pyraquant_amd import int8_exec as E
+
+    l1t = _l1(K, 32, torch.bfloat16, 7 + K).t().contiguous()
+    got = E.pack_lowrank_l1t(l1t.to(cuda))
+    ref = _fragment_order_np(bits(l1t).reshape(32, K))
+    assert np.array_equal(bits(got).reshape(32, K), ref)
+    assert np.array_equal(np.sort(ref.ravel()), np.sort(bits(l1t).ravel()))
+    assert E.pack_lowrank_l1t(torch.zeros(64, K, dtype=torch.bfloat16, device=cuda)) is None
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K", [(1, 3072), (17, 1280), (4096, 3072), (1000, 1024), (300, 2048), (65, 2560),
+                                 (20000, 3072)])
+def test_quant_rows_lowrank_fragment_order_identical(cuda, dtype, M, K):
+    """Codes, scales and t are bit-identical whether the one-pass kernel reads l1t or its fragment-order copy,
+    plain and through a routed gather."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_x
+
+    x = make_x(M, K, dtype, seed=3 * M + K, device=cuda)
+    l1t = _l1(K, 32, dtype, K + 1).t().contiguous().to(cuda)
+    l1f = E.pack_lowrank_l1t(l1t)
+    assert l1f is not None
+    idx = torch.randint(0, M, (max(1, M // 3),), generator=torch.Generator().manual_seed(M), dtype=torch.int32)
+    for idx in (None, idx.to(cuda)):
+        a = E.quant_rows_lowrank(x, l1t, idx)
+        b = E.quant_rows_lowrank(x, l1t, idx, l1f)
+        for u, v in zip(a, b):   # codes (int8), scales (fp32 bits), t (16-bit bits)
+            as_int = {1: torch.int8, 2: torch.int16, 4: torch.int32}[u.element_size()]
+            assert torch.equal(u.view(as_int), v.view(as_int))
+
+
+def test_int8linear_keeps_fragment_order_through_casts(cuda):
+    """Int8Linear packs lr_At_frag at conversion where the order exists (K = 3072, rank 32) and not otherwise
+    (K = 4096); a module-wide cast carries it with lr_At, and the forward's output is the same with or without it."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    q = E.Int8Linear(make_linear(3072, 640, 32, True, seed=5), device=cuda)
+    assert q.lr_At_frag is not None and "lr_At_frag" not in q.state_dict()
+    assert E.Int8Linear(make_linear(4096, 640, 32, True, seed=5), device=cuda).lr_At_frag is None
+    x = make_x(333, 3072, torch.bfloat16, seed=9, device=cuda)
+    y = q(x)
+    frag = q.lr_At_frag
+    q.lr_At_frag = None
+    y_plain = q(x)
+    q.lr_At_frag = frag
+    assert torch.equal(y.view(torch.int16), y_plain.view(torch.int16))
+    q.half()
+    assert q.lr_At_frag.dtype == torch.float16 and q._lr_frag() is not None
+    xh = x.half()
+    yh = q(xh)
+    q.lr_At_frag = None
+    assert torch.equal(yh.view(torch.int16), q(xh).view(torch.int16))

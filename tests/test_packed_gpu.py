@@ -146,7 +146,7 @@ def test_int8linear_packed_path(oracle, cuda, cfg, M):
     mx, mean = rel_errors(oracle.to_f32(bits(y), 0), o["y"])
     assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
     xq, sx = E.quant_rows(x)
-    _, _, t = E.quant_rows_lowrank(x, q.lr_At)   # the low-rank rows the forward computed
+    _, _, t = E.quant_rows_lowrank(x, q.lr_At, None, q._lr_frag())   # the low-rank rows the forward computed
     ref = E._gemm(xq, sx, q.weight_int8, q.w_scale, 0, q.bias, t, q.lr_Bt, torch.bfloat16)
     assert torch.equal(y, ref)
 

@@ -24,7 +24,7 @@ def _args(q, x):
     Re = 0 if q.lr_Bt is None else q.lr_Bt.shape[1]
     p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
     return [p(x), _lib.dtype_code(x.dtype), x.shape[0], x.shape[1], x.stride(0), p(q.weight_packed), p(q._scale_k()),
-            q.group_size, p(q.bias), p(q.lr_At), R, p(q.lr_Bt), Re]
+            q.group_size, p(q.bias), p(q.lr_At), p(q._lr_frag()), R, p(q.lr_Bt), Re]
 
 
 def _run_both(L, q, x):
