@@ -149,7 +149,7 @@ int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
  * K is one of 1024, 1280, 2048, 2560, 3072, rows are 16-byte aligned (ldx % 8 == 0) and every x byte offset fits
  * 30 bits; other shapes run the two kernels. l1t [R, K] contiguous, same dtype as x; t [M, R] with row stride ldt.
  * l1f: NULL, or the same matrix in the one-pass kernel's fragment order (pq_pack_lowrank_l1t, 16-byte aligned),
- * which that kernel then reads instead of l1t (contiguous 1 KB register loads: 15.1 -> 12.7 us at M = 4096,
+ * which that kernel then reads instead of l1t (contiguous 1 KB register loads: 15.8 -> 12.8 us at M = 4096,
  * K = 3072); results are identical either way, and l1t is still required (the other paths read it).
  */
 int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,

@@ -412,7 +412,7 @@ __device__ __forceinline__ int row_byte_offset(int64_t m, int64_t M, const int32
 // The l1t slice comes from l1f when given: the same matrix in fragment order (pack_lowrank_l1t_kernel), where each
 // of the wave's 4 NC register loads is one contiguous 1 KB piece. From row-major l1t each load touches 16 rows at
 // half a cache line apiece; with one batch per workgroup (c0: M = 4096, 256 batches) the whole 192 KB slice set is
-// on the critical path, and the fragment order takes the pass from 15.1 to 12.7 us.
+// on the critical path, and the fragment order takes the pass from 15.8 to 12.8 us.
 // W = 16 where K allows it (K % 1024 == 0), else 8, else 4: the batch's work is spread over more waves while the
 // single LDS batch buffer (the memory pipeline) stays the same (c1: 143 -> 130 us from W = 4 to 16).
 // K assignment inside the 64-wide K block c of a slice (MFMA steps 2c and 2c + 1): lane group g covers
@@ -459,15 +459,6 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
 
   v4u xv[NS];
   const uint8_t* xrow = xs + r * PITCH + 2 * (k0 + 16 * g);
-  int b = blockIdx.x;
-#pragma unroll
-  for (int j = 0; j < 16 / W; ++j) xoff[j] = row_off(b, j);
-  dma();
-#pragma unroll
-  for (int j = 0; j < 16 / W; ++j) xoff[j] = row_off(b + G, j);
-  // The first batch's DMA is issued before the l1t slice is loaded: its HBM latency then overlaps the l1t reads
-  // instead of queueing behind them (at small M every workgroup runs a single batch, so nothing else hides it).
-  __builtin_amdgcn_sched_barrier(0);
   // l1t fragments of this wave's slice: lf[h][2 c + e] = l1t[16 h + r][k0 + 64 c + 16 g + 8 e .. + 8]
   // (in l1f: 16-byte piece ((wave * 2 + h) * NS + 2 c + e) * 64 + lane)
   v4u lf[2][NS];
@@ -485,17 +476,24 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
         lf[h][i] = *reinterpret_cast<const v4u*>(l1t + (int64_t)(16 * h + r) * K + k0 + 64 * (i >> 1) + 16 * g +
                                                  8 * (i & 1));
   }
-  // One batch. The first batch's DMA is followed only by the l1t loads (4 NC of them), which may stay in flight: the
-  // low-rank MFMAs that need them come after the codes, so the l1t reads land under that work (at small M every
-  // workgroup runs one batch and nothing else would hide them). The first batch is peeled off the loop, so that the
-  // compiler's wait for the l1t registers sits at those MFMAs rather than before the loop. Later DMAs are followed
-  // by the previous batch's stores, a count that differs between waves, so those waits are for everything.
+  // The l1t loads go out before the first batch's DMA: at small M every workgroup runs a single batch, whose x
+  // arrives from HBM later than l1t from L2, so the slice is in registers by the time the batch is (measured at
+  // M = 4096, K = 3072: 13.0 -> 11.7 us against issuing the DMA first).
+  __builtin_amdgcn_sched_barrier(0);
+  int b = blockIdx.x;
+#pragma unroll
+  for (int j = 0; j < 16 / W; ++j) xoff[j] = row_off(b, j);
+  dma();
+#pragma unroll
+  for (int j = 0; j < 16 / W; ++j) xoff[j] = row_off(b + G, j);
+  // One batch. Its DMA was the last memory operation this wave issued before the batch (after the l1t loads, or
+  // after the previous batch's stores), so the wait is for everything. The first batch is peeled off the loop (the
+  // `first` tag only makes it a separate copy of the code): with every batch in one loop the compiler runs out of
+  // the 128 VGPRs of a 16-wave workgroup by one, spills it, and its reload inside the loop waits with vmcnt(0), i.e.
+  // also for the next batch's DMA in flight, which takes the c1 pass from 118 to 132 us.
   auto batch = [&](int b, auto first) {
-    if constexpr (decltype(first)::value) {
-      wait_vmcnt<4 * NC>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    (void)first;
+    wait_vmcnt<0>();
     __syncthreads();   // every wave's DMA of batch b has landed
 #pragma unroll
     for (int i = 0; i < NS; ++i) xv[i] = *reinterpret_cast<const v4u*>(xrow + 128 * (i >> 1) + 16 * (i & 1));
@@ -540,7 +538,7 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
       *reinterpret_cast<v4u*>(qp + k64_offset(m, k0 + 64 * c + 16 * g, K / 64)) = v4u{lo.x, lo.y, hi.x, hi.y};
     }
     if (wave == 0 && g == 0 && m < M) s[m] = sc;
-    // low rank: partial t over the slice, after the codes so that the first batch's l1t loads land under them
+    // low rank: partial t over the slice
     v4f acc[2] = {v4f{}, v4f{}};
 #pragma unroll
     for (int i = 0; i < NS; ++i)
