@@ -78,11 +78,12 @@ const char* pq_last_error(void);
  *   s[m] = a / 127.0f                                    (IEEE fp32 division, round to nearest even)
  *   q[m, k] = clamp(rint(x[r, k] / s[m]), -127, 127)     (IEEE fp32 division, rint = half to even)
  * which is the reference's torch restatement (deploy/int8_exec.py:508-509). q is [M, K] contiguous.
- * row_idx entries must lie in [0, rows of x); they are not range-checked on the device.
+ * x has x_rows rows (x_rows >= M without row_idx). A row_idx entry outside [0, x_rows) reads as a row of zeros
+ * (codes 0, s = fl(1e-8) / 127) instead of memory past x; torch's index ops would raise there.
  * Inputs must be finite. Any K >= 1 and ldx >= K are accepted; 16-byte aligned x with ldx % 8 == 0 and
  * K % 8 == 0 takes the vectorised kernel, anything else a per-element kernel with the same results.
  */
-int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
                   const int32_t* row_idx, int8_t* q, float* s, hipStream_t stream);
 
 /*
@@ -101,7 +102,8 @@ int pq_quant_weight(const float* w, int64_t N, int64_t K, int64_t ldw, int64_t g
  * Replaces `t = x2.to(self.lr_A.dtype) @ self.lr_A` (deploy/int8_exec.py:390; also :403).
  * x is [x_rows, ldx] (the rows row_idx may name; without row_idx x_rows >= M). x and l1t must have the same dtype.
  * l1t is lr_A transposed ([R, K], K-contiguous). R in {32, 64, 96, 128}, K % 8 == 0, 16-byte aligned x / l1t / t,
- * ldx % 8 == 0, ldt % 8 == 0. row_idx as in pq_quant_rows (the routed gather), or NULL. K % 64 == 0 and R <= 64 take
+ * ldx % 8 == 0, ldt % 8 == 0. row_idx as in pq_quant_rows (the routed gather; entries outside [0, x_rows) read as zero
+ * rows), or NULL. K % 64 == 0 and R <= 64 take
  * the LDS-DMA kernel (x streamed once in whole 128-byte row segments); other shapes a per-row-fragment kernel.
  */
 int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
@@ -116,7 +118,9 @@ int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t 
  *   if bias: y += bias[n]
  *   c[o, n] = round_to_out_dtype(y), o = out_row_idx ? out_row_idx[m] : m (routed scatter)
  * The int32 accumulator never leaves registers. Rows of c not named by out_row_idx are not written,
- * so they keep whatever the caller left there (the routed executor's cached canvas).
+ * so they keep whatever the caller left there (the routed executor's cached canvas). With out_row_idx, c has
+ * c_rows rows, and a row whose index lies outside [0, c_rows) is not written (torch's index ops would raise); without
+ * it c has M rows and c_rows is ignored.
  * Replaces `int8_gemm_fused` / `_int8_gemm_fused_kernel_impl` (deploy/int8_exec.py:144-183, 202-212),
  * `int8_gemm_lr` / `_int8_gemm_lr_impl` (deploy/int8_exec.py:272-314, 327-336; epilogue order
  * :303-309), the SDXL narrow-N variant (deploy/run_sdxl_latency.py:131-140, 173-195). The group-32
@@ -124,12 +128,12 @@ int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t 
  * Requirements: K % 64 == 0, N % 64 == 0, M >= 1; a, w 16-byte aligned with lda, ldw % 16 == 0;
  * c 8-byte aligned with ldc % 4 == 0 and ldc < 2^31; t, l2t 16-byte aligned with ldt % 8 == 0, ldt <= 2^22,
  * R in {16, 32, 64}; group 32 needs N * K < 2^33 (its scales are read at 32-bit buffer offsets);
- * lr_dtype and out_dtype are PQ_BF16 or PQ_F16; out_row_idx entries unique and in range.
+ * lr_dtype and out_dtype are PQ_BF16 or PQ_F16; out_row_idx entries unique (two rows naming one row of c race).
  */
 int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
                  const float* s_row, const float* s_w, int64_t group, const float* bias,
                  const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
-                 void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx,
+                 void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows,
                  int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 /*
@@ -179,8 +183,8 @@ int pq_pack_lowrank_l1t(const void* l1t, int32_t dtype, int64_t R, int64_t K, vo
  */
 int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w, int64_t group,
                         const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
-                        void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t M, int64_t N,
-                        int64_t K, hipStream_t stream);
+                        void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows,
+                        int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 /*
  * Bytes of workspace pq_int8_linear needs for M rows, K inputs and R columns of t (R = 0: no low-rank branch):
@@ -238,7 +242,7 @@ int pq_pack_k64(const int8_t* src, int64_t R, int64_t K, int64_t lds, int8_t* ds
  * aligned; padding rows zero) instead of row-major; s and every other argument as pq_quant_rows. K % 64 == 0.
  * Replaces `quant_rows` (deploy/int8_exec.py:216-230) on the Int8Linear forward path (:391).
  */
-int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
                          const int32_t* row_idx, int8_t* qp, float* s, hipStream_t stream);
 
 /*

@@ -52,17 +52,17 @@ _i32 = ctypes.c_int32
 _SIGNATURES = {
     "pq_abi_version": ([], ctypes.c_int),
     "pq_last_error": ([], ctypes.c_char_p),
-    "pq_quant_rows": ([_p, _i32, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
+    "pq_quant_rows": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
     "pq_quant_weight": ([_p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "pq_lowrank_down": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p], ctypes.c_int),
-    "pq_int8_gemm": ([_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p,
+    "pq_int8_gemm": ([_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p, _i64,
                       _i64, _i64, _i64, _p], ctypes.c_int),
     "pq_int8_gemm_i32": ([_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
     "pq_int8_gemm_packed": ([_p, _p, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p, _i64, _i64, _i64,
-                             _p],
+                             _i64, _p],
                             ctypes.c_int),
     "pq_pack_k64": ([_p, _i64, _i64, _i64, _p, _p], ctypes.c_int),
-    "pq_quant_rows_packed": ([_p, _i32, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
+    "pq_quant_rows_packed": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
     "pq_quant_rows_lowrank": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _p, _p, _i64, _p], ctypes.c_int),
     "pq_pack_lowrank_l1t": ([_p, _i32, _i64, _i64, _p, _p], ctypes.c_int),
     "pq_dequant_epilogue": ([_p, _p, _p, _p, _p, _i64, _i32, _i64, _i64, _p], ctypes.c_int),

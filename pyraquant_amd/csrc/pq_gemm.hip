@@ -54,6 +54,7 @@ struct GemmArgs {
   const uint16_t* l2t;
   void* c;
   const int32_t* out_row_idx;
+  int64_t c_rows;   // rows of c a scattered row may name: a row index outside [0, c_rows) is not written
   int64_t lda, ldw, ldt, ldc;
   int M, N, K, R;
   int tiles_m, tiles_n;
@@ -210,7 +211,10 @@ struct Epilogue {
         const int ldc = (int)p.ldc;
         uint16_t* const cn = static_cast<uint16_t*>(p.c) + n;
         uint16_t* const cm = cn + (int64_t)(mbase + lr_) * ldc;
-        auto valid = [&](int s0) { return nvalid && mbase + j * 32 + s0 + lr_ < p.M; };
+        auto valid = [&](int s0) {
+          return nvalid && mbase + j * 32 + s0 + lr_ < p.M &&
+                 (!p.out_row_idx || (uint64_t)(int64_t)orows[mloc + j * 32 + s0 + lr_] < (uint64_t)p.c_rows);
+        };
         auto dst_of = [&](int s0) {
           return p.out_row_idx ? cn + (int64_t)orows[mloc + j * 32 + s0 + lr_] * ldc : cm + (int64_t)(j * 32 + s0) * ldc;
         };
@@ -364,7 +368,7 @@ struct Epilogue {
         const int row = s0 + lr_;
         const int m = mbase + row;
         v4u v = *reinterpret_cast<const v4u*>(stage + row * kPitch + lc * 16);
-        if (nvalid && m < p.M) {
+        if (nvalid && m < p.M && (!p.out_row_idx || (uint64_t)(int64_t)srow[row] < (uint64_t)p.c_rows)) {
           uint16_t* const dst = p.out_row_idx ? cn + (int64_t)srow[row] * ldc : cm + (int64_t)s0 * ldc;
           if constexpr (ACC) v = add_16x8<ODT>(*reinterpret_cast<const v4u*>(dst), v);   // accumulate into c
           if constexpr (NTS) {
@@ -817,11 +821,13 @@ using namespace pq;
 extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw, const float* s_row,
                             const float* s_w, int64_t group, const float* bias, const void* t, int64_t ldt,
                             const void* l2t, int64_t R, int32_t lr_dtype, void* c, int64_t ldc,
-                            int32_t out_dtype, const int32_t* out_row_idx, int64_t M, int64_t N, int64_t K,
-                            hipStream_t stream) {
+                            int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows, int64_t M, int64_t N,
+                            int64_t K, hipStream_t stream) {
   int st = check_common(a, lda, w, ldw, M, N, K, "pq_int8_gemm");
   if (st != PQ_OK) return st;
   if (M == 0) return PQ_OK;
+  if (out_row_idx && c_rows < 1)
+    return set_error(PQ_ESHAPE, "pq_int8_gemm: a scatter needs the rows of c (c_rows=%lld)", (long long)c_rows);
   if (!s_row || !s_w || !c) return set_error(PQ_EINVAL, "pq_int8_gemm: null s_row / s_w / c");
   if (group != 0 && group != 32) return set_error(PQ_ESHAPE, "pq_int8_gemm: group must be 0 or 32, got %lld", (long long)group);
   if (group == 32 && (K / 32) * N * 4 > kOOB - 4096)
@@ -844,7 +850,7 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
   GemmArgs args{};
   args.a = a; args.w = w; args.s_row = s_row; args.s_w = s_w; args.bias = bias;
   args.t = static_cast<const uint16_t*>(t); args.l2t = static_cast<const uint16_t*>(l2t);
-  args.c = c; args.out_row_idx = out_row_idx;
+  args.c = c; args.out_row_idx = out_row_idx; args.c_rows = c_rows;
   args.lda = lda; args.ldw = ldw; args.ldt = ldt; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K; args.R = (int)R;
   if (group == 32) return dispatch_dtypes<false, kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
@@ -871,7 +877,8 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
 extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
                                    int64_t group, const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R,
                                    int32_t lr_dtype, void* c, int64_t ldc, int32_t out_dtype,
-                                   const int32_t* out_row_idx, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+                                   const int32_t* out_row_idx, int64_t c_rows, int64_t M, int64_t N, int64_t K,
+                                   hipStream_t stream) {
   const bool accumulate = (out_dtype & PQ_ACCUMULATE) != 0;
   out_dtype &= ~PQ_ACCUMULATE;
   if (M < 0 || N < 1 || K < 1) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: bad shape");
@@ -898,6 +905,8 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
     return launch_dma<2, 2, 2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
   }
   if (!s_row || !s_w) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null s_row / s_w");
+  if (out_row_idx && c_rows < 1)
+    return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: a scatter needs the rows of c (c_rows=%lld)", (long long)c_rows);
   if (group != 0 && group != 32)
     return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: group must be 0 or 32, got %lld", (long long)group);
   if (group == 32 && (K / 32) * N * 4 > kOOB - 4096)
@@ -919,7 +928,7 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
   }
   args.s_row = s_row; args.s_w = s_w; args.bias = bias;
   args.t = static_cast<const uint16_t*>(t); args.l2t = static_cast<const uint16_t*>(l2t);
-  args.out_row_idx = out_row_idx;
+  args.out_row_idx = out_row_idx; args.c_rows = c_rows;
   args.ldt = ldt; args.ldc = ldc; args.R = (int)R;
   if (group == 32) return dispatch_dtypes<true, kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
   if (accumulate) return dispatch_dtypes<true, kModeChannel, true>(args, has_lr, lr_dtype, out_dtype, stream);

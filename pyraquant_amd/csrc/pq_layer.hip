@@ -40,10 +40,10 @@ static int run_layer(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64
   float* const s = reinterpret_cast<float*>(ws + sl.scales);
   void* const t = R ? static_cast<void*>(ws + sl.t) : nullptr;
   int st = R ? pq_quant_rows_lowrank(x, x_dtype, M, K, ldx, M, nullptr, l1t, l1f, R, q, s, t, R, stream)
-             : pq_quant_rows_packed(x, x_dtype, M, K, ldx, nullptr, q, s, stream);
+             : pq_quant_rows_packed(x, x_dtype, M, K, ldx, M, nullptr, q, s, stream);
   if (st != PQ_OK) return st;
   return pq_int8_gemm_packed(q, w_packed, s, s_w, group, bias, R ? t : nullptr, R, R ? l2t : nullptr, Re, x_dtype, y,
-                             ldy, x_dtype, nullptr, M, N, K, stream);
+                             ldy, x_dtype, nullptr, 0, M, N, K, stream);
 }
 
 int check_layer(int64_t M, int64_t K, int64_t N, int64_t R, int64_t Re, const void* l1t, const void* l2t,

@@ -83,11 +83,11 @@ __device__ __forceinline__ float absmax_from_bits(uint32_t mag16) {
 
 // Vectorised quantizer: one wave per row, CH 16-byte chunks per lane, 4 rows per 256-thread block.
 // PACKED: codes go to the packed K64 layout (8-byte stores at k64_offset), and the waves of the padding rows
-// M .. 16 * ceil(M / 16) - 1 write zeros there.
+// M .. 16 * ceil(M / 16) - 1 write zeros there. A gathered source row outside [0, x_rows) reads as zeros.
 template <int DT, int CH, bool PACKED>
 __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
-    int8_t* __restrict__ q, float* __restrict__ s) {
+    int8_t* __restrict__ q, float* __restrict__ s, int64_t x_rows) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nvec = K >> 3;
@@ -102,12 +102,13 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
   }
   if (m >= M) return;
   const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
-  const v4u* __restrict__ xr = reinterpret_cast<const v4u*>(x + src * ldx);
+  const bool live = src >= 0 && src < x_rows;
+  const v4u* __restrict__ xr = reinterpret_cast<const v4u*>(x + (live ? src : 0) * ldx);
   v4u v[CH];
 #pragma unroll
   for (int c = 0; c < CH; ++c) {
     const int idx = c * 64 + lane;
-    v[c] = idx < nvec ? __builtin_nontemporal_load(xr + idx) : v4u{0u, 0u, 0u, 0u};
+    v[c] = live && idx < nvec ? __builtin_nontemporal_load(xr + idx) : v4u{0u, 0u, 0u, 0u};
   }
   us2 mx2 = {0, 0};
 #pragma unroll
@@ -138,11 +139,12 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
   if (lane == 0) s[m] = sc;
 }
 
-// Per-element quantizer for unaligned rows or odd K: one wave per row, two sweeps over the row.
+// Per-element quantizer for unaligned rows or odd K: one wave per row, two sweeps over the row (a gathered source row
+// outside [0, x_rows) reads as zeros).
 template <int DT, bool PACKED>
 __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
-    int8_t* __restrict__ q, float* __restrict__ s) {
+    int8_t* __restrict__ q, float* __restrict__ s, int64_t x_rows) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if constexpr (PACKED) {
@@ -155,10 +157,11 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
   }
   if (m >= M) return;
   const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
-  const uint16_t* __restrict__ xr = x + src * ldx;
+  const bool live = src >= 0 && src < x_rows;
+  const uint16_t* __restrict__ xr = x + (live ? src : 0) * ldx;
   uint32_t mx = 0;
   for (int k = lane; k < K; k += 64) {
-    const uint32_t b = xr[k] & 0x7fffu;
+    const uint32_t b = live ? xr[k] & 0x7fffu : 0u;
     mx = b > mx ? b : mx;
   }
   mx = wave_max_u32(mx);
@@ -166,7 +169,7 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
   const float sc = __fdiv_rn(a, 127.0f);
   int8_t* __restrict__ qr = q + m * (int64_t)K;
   for (int k = lane; k < K; k += 64) {
-    const float f = lo16_to_f32<DT>(xr[k]);
+    const float f = live ? lo16_to_f32<DT>(xr[k]) : 0.0f;
     const int8_t code = (int8_t)(__float_as_uint(code_exact(f, sc)) & 0xffu);
     if constexpr (PACKED) {
       q[k64_offset(m, k, K >> 6)] = code;
@@ -178,7 +181,7 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
 }
 
 template <int DT, bool PACKED>
-int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t* row_idx, int8_t* q,
+int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t x_rows, const int32_t* row_idx, int8_t* q,
                  float* s, hipStream_t stream) {
   const dim3 block(256);
   const int64_t rows = PACKED ? ((M + 15) & ~15LL) : M;
@@ -191,7 +194,7 @@ int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t
 #define PQ_QCASE(C)                                                                                       \
   if (need <= C) {                                                                                        \
     hipLaunchKernelGGL((quant_rows_vec_kernel<DT, C, PACKED>), grid, block, 0, stream, xp, ldx, (int)K, M, \
-                       row_idx, q, s);                                                                    \
+                       row_idx, q, s, x_rows);                                                            \
     return check_launch("quant_rows_vec");                                                                \
   }
     PQ_QCASE(1) PQ_QCASE(2) PQ_QCASE(3) PQ_QCASE(4) PQ_QCASE(5) PQ_QCASE(6) PQ_QCASE(8) PQ_QCASE(10)
@@ -199,7 +202,7 @@ int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t
 #undef PQ_QCASE
   }
   hipLaunchKernelGGL((quant_rows_scalar_kernel<DT, PACKED>), grid, block, 0, stream, xp, ldx, (int)K, M, row_idx,
-                     q, s);
+                     q, s, x_rows);
   return check_launch("quant_rows_scalar");
 }
 
@@ -210,14 +213,15 @@ int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, const int32_t
 template <int DT, int RB>
 __global__ __launch_bounds__(256) void lowrank_down_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
-    const uint16_t* __restrict__ l1t, uint16_t* __restrict__ t, int64_t ldt) {
+    const uint16_t* __restrict__ l1t, uint16_t* __restrict__ t, int64_t ldt, int64_t x_rows) {
   const int lane = threadIdx.x & 63;
   const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 32;
   if (r0 >= M) return;
   int64_t mrow = r0 + (lane & 31);
   const int64_t mcl = mrow < M ? mrow : M - 1;
   const int64_t src = row_idx ? (int64_t)row_idx[mcl] : mcl;
-  const uint16_t* __restrict__ xr = x + src * ldx + (lane >> 5) * 8;
+  const bool live = src >= 0 && src < x_rows;   // a gathered row outside x reads as zeros
+  const uint16_t* __restrict__ xr = x + (live ? src : 0) * ldx + (lane >> 5) * 8;
   const uint16_t* __restrict__ lr = l1t + (int64_t)(lane & 31) * K + (lane >> 5) * 8;
   v16f acc[RB];
 #pragma unroll
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(256) void lowrank_down_kernel(
   const int koff = (lane >> 5) * 8;
   for (int k0 = 0; k0 < K; k0 += 16) {
     const bool in = (k0 + koff) < K;
-    const v4u xa = in ? *reinterpret_cast<const v4u*>(xr + k0) : v4u{0u, 0u, 0u, 0u};
+    const v4u xa = in && live ? *reinterpret_cast<const v4u*>(xr + k0) : v4u{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
       const v4u lb = in ? *reinterpret_cast<const v4u*>(lr + (int64_t)b * 32 * K + k0) : v4u{0u, 0u, 0u, 0u};
@@ -325,7 +329,8 @@ __global__ __launch_bounds__(256) void lowrank_down_dma_kernel(
   for (int i = 0; i < 4; ++i) {
     const int64_t m = min(m0 + (wave * 4 + i) * 8 + (lane >> 3), M - 1);
     const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
-    vx[i] = (int)(src * ldx * 2) + (((lane & 7) ^ (lane >> 3) ^ (i & 1)) << 4);
+    // a gathered row outside x: offset kOOB, the DMA loads zeros
+    vx[i] = src >= 0 && src < x_rows ? (int)(src * ldx * 2) + (((lane & 7) ^ (lane >> 3) ^ (i & 1)) << 4) : kOOB;
   }
   // l1t: instruction j fills rows 32 j + 8 wave + lane / 8; row % 8 = lane / 8 and row / 8 % 2 = wave % 2
   const int vl = ((wave * 8 + (lane >> 3)) * K) * 2 + (((lane & 7) ^ (lane >> 3) ^ (wave & 1)) << 4);
@@ -393,9 +398,13 @@ __global__ __launch_bounds__(256) void lowrank_down_dma_kernel(
   }
 }
 
-// Byte offset of output row m's source row in x (x_rows * ldx * 2 < 2^30), or kOOB past M (a DMA that loads nothing).
-__device__ __forceinline__ int row_byte_offset(int64_t m, int64_t M, const int32_t* __restrict__ row_idx, int64_t ldx) {
-  return m < M ? (int)((row_idx ? (int64_t)row_idx[m] : m) * ldx * 2) : kOOB;
+// Byte offset of output row m's source row in x (x_rows * ldx * 2 < 2^30), or kOOB (a DMA that loads zeros) past M
+// and for a gathered row outside [0, x_rows).
+__device__ __forceinline__ int row_byte_offset(int64_t m, int64_t M, const int32_t* __restrict__ row_idx, int64_t ldx,
+                                               int64_t x_rows) {
+  if (m >= M) return kOOB;
+  const int64_t src = row_idx ? (int64_t)row_idx[m] : m;
+  return src >= 0 && src < x_rows ? (int)(src * ldx * 2) : kOOB;
 }
 
 // ---- fused quantizer + low-rank down-projection (one read of x) ----------------------------------------------
@@ -444,7 +453,9 @@ __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
   // is read one batch ahead of its DMA, so the scalar load completes under the previous batch's work instead of
   // delaying the DMA issue.
   int xoff[16 / W];
-  auto row_off = [&](int bb, int j) { return row_byte_offset((int64_t)bb * 16 + wave * (16 / W) + j, M, row_idx, ldx); };
+  auto row_off = [&](int bb, int j) {
+    return row_byte_offset((int64_t)bb * 16 + wave * (16 / W) + j, M, row_idx, ldx, x_rows);
+  };
   auto dma = [&]() {
 #pragma unroll
     for (int j = 0; j < 16 / W; ++j) {
@@ -627,7 +638,7 @@ constexpr int kWideRedPitch = 36;             // floats per row of the partial-s
 
 template <int DT, int NCH>   // NCH = K / 512: 16-byte chunks per lane per row, and slabs
 __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, int64_t M, const int32_t* __restrict__ row_idx,
+    const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int64_t M, const int32_t* __restrict__ row_idx,
     const uint16_t* __restrict__ l1t, int8_t* __restrict__ qp, float* __restrict__ s, uint16_t* __restrict__ t,
     int64_t ldt, int nbatch) {
   constexpr int K = 512 * NCH;
@@ -653,13 +664,17 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
                                                voff_l + i * K * 2, e * kWideSlab * 2, 0, 0);
   };
 
-  // Row rho of this wave in batch bb: its source row in x (row 0 for a padding row past M, whose loads are
-  // harmless and whose data is cleared before use). Wave-uniform: the row bases stay in scalar registers and each
-  // lane adds its own 16-byte offset.
-  auto src_row = [&](int bb, int rho) -> const v4u* {
+  // Row rho of this wave in batch bb: its source row in x, or -1 for a padding row past M and a gathered row outside
+  // [0, x_rows) (both read as zeros: row 0 is loaded, harmlessly, and the data cleared before use). Wave-uniform:
+  // the row bases stay in scalar registers and each lane adds its own 16-byte offset.
+  auto src_of = [&](int bb, int rho) -> int64_t {
     const int64_t m = (int64_t)bb * 16 + 2 * wave + rho;
-    const int64_t src = m >= M ? 0 : (row_idx ? (int64_t)row_idx[m] : m);
-    return reinterpret_cast<const v4u*>(x + src * ldx);
+    const int64_t src = m >= M ? -1 : (row_idx ? (int64_t)row_idx[m] : m);
+    return src >= 0 && src < x_rows ? src : -1;
+  };
+  auto src_row = [&](int bb, int rho) -> const v4u* {
+    const int64_t src = src_of(bb, rho);
+    return reinterpret_cast<const v4u*>(x + (src < 0 ? 0 : src) * ldx);
   };
   // this lane's byte offset inside a row's packed K64 codes, for the rows 2 w (rho = 0) and 2 w + 1 of a batch
   int qlane[2];
@@ -683,7 +698,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
     for (int rho = 0; rho < 2; ++rho) {
       mrow[rho] = (int64_t)b * 16 + 2 * wave + rho;
       xn[rho] = src_row(bn < nbatch ? bn : b, rho);
-      if (mrow[rho] >= M) {   // a padding row: its codes must be zero
+      if (src_of(b, rho) < 0) {   // a padding row or a gathered row outside x: it quantizes as zeros
 #pragma unroll
         for (int c = 0; c < NCH; ++c) v[rho][c] = v4u{0u, 0u, 0u, 0u};
       }
@@ -829,19 +844,21 @@ extern "C" int pq_abi_version(void) { return PQ_ABI_VERSION; }
 
 extern "C" const char* pq_last_error(void) { return pq::g_err; }
 
-extern "C" int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+extern "C" int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
                              const int32_t* row_idx, int8_t* q, float* s, hipStream_t stream) {
   if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_rows: bad shape M=%lld K=%lld", (long long)M, (long long)K);
   if (M == 0) return PQ_OK;
   if (!x || !q || !s) return set_error(PQ_EINVAL, "pq_quant_rows: null pointer");
   if (ldx < K) return set_error(PQ_ESHAPE, "pq_quant_rows: ldx=%lld < K=%lld", (long long)ldx, (long long)K);
   if (K > (1LL << 30) || M > (1LL << 40)) return set_error(PQ_ESHAPE, "pq_quant_rows: shape too large");
-  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, false>(x, M, K, ldx, row_idx, q, s, stream);
-  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, false>(x, M, K, ldx, row_idx, q, s, stream);
+  if (x_rows < 1 || (!row_idx && x_rows < M))
+    return set_error(PQ_ESHAPE, "pq_quant_rows: x_rows=%lld must cover the rows read", (long long)x_rows);
+  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, false>(x, M, K, ldx, x_rows, row_idx, q, s, stream);
+  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, false>(x, M, K, ldx, x_rows, row_idx, q, s, stream);
   return set_error(PQ_EDTYPE, "pq_quant_rows: unsupported dtype code %d", (int)x_dtype);
 }
 
-extern "C" int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
+extern "C" int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
                                     const int32_t* row_idx, int8_t* qp, float* s, hipStream_t stream) {
   if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: bad shape M=%lld K=%lld", (long long)M, (long long)K);
   if (K % 64 != 0) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: K=%lld must be a multiple of 64", (long long)K);
@@ -850,8 +867,10 @@ extern "C" int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, i
   if ((uintptr_t)qp % 16) return set_error(PQ_EALIGN, "pq_quant_rows_packed: qp must be 16-byte aligned");
   if (ldx < K) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: ldx=%lld < K=%lld", (long long)ldx, (long long)K);
   if (K > (1LL << 30) || M > (1LL << 40)) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: shape too large");
-  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, true>(x, M, K, ldx, row_idx, qp, s, stream);
-  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, true>(x, M, K, ldx, row_idx, qp, s, stream);
+  if (x_rows < 1 || (!row_idx && x_rows < M))
+    return set_error(PQ_ESHAPE, "pq_quant_rows_packed: x_rows=%lld must cover the rows read", (long long)x_rows);
+  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, true>(x, M, K, ldx, x_rows, row_idx, qp, s, stream);
+  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, true>(x, M, K, ldx, x_rows, row_idx, qp, s, stream);
   return set_error(PQ_EDTYPE, "pq_quant_rows_packed: unsupported dtype code %d", (int)x_dtype);
 }
 
@@ -889,7 +908,7 @@ extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t 
 #define PQ_LRCASE(D, RB)                                                                                    \
   if (dtype == D && R == RB * 32) {                                                                         \
     hipLaunchKernelGGL((lowrank_down_kernel<D, RB>), grid, block, 0, stream, xp, ldx, (int)K, M, row_idx,  \
-                       lp, tp, ldt);                                                                        \
+                       lp, tp, ldt, x_rows);                                                                \
     return check_launch("lowrank_down");                                                                    \
   }
   PQ_LRCASE(PQ_BF16, 1) PQ_LRCASE(PQ_BF16, 2) PQ_LRCASE(PQ_BF16, 3) PQ_LRCASE(PQ_BF16, 4)
@@ -915,7 +934,7 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
                      (uintptr_t)qp % 16 == 0 && (x_dtype == PQ_BF16 || x_dtype == PQ_F16);
   // wide rows: one read of x through registers (quant_lowrank_wide_kernel)
   const bool wide = !fused && R == 32 && K % 2048 == 0 && K >= 4096 && K <= 12288 && ldx >= K && ldx % 8 == 0 &&
-                    ldt >= R && ldt % 2 == 0 && (row_idx || x_rows >= M) && (uintptr_t)x % 16 == 0 &&
+                    ldt >= R && ldt % 2 == 0 && x_rows >= 1 && (row_idx || x_rows >= M) && (uintptr_t)x % 16 == 0 &&
                     (uintptr_t)l1t % 16 == 0 && (uintptr_t)t % 4 == 0 && (uintptr_t)qp % 16 == 0 &&
                     (x_dtype == PQ_BF16 || x_dtype == PQ_F16);
   if (wide) {
@@ -926,8 +945,8 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
     uint16_t* tp = static_cast<uint16_t*>(t);
 #define PQ_QWCASE(D, NCH)                                                                                      \
     if (x_dtype == D && K == 512 * NCH) {                                                                      \
-      hipLaunchKernelGGL((quant_lowrank_wide_kernel<D, NCH>), grid, dim3(64 * kWideWaves), 0, stream, xp, ldx, M, \
-                         row_idx, lp, qp, s, tp, ldt, nbatch);                                                 \
+      hipLaunchKernelGGL((quant_lowrank_wide_kernel<D, NCH>), grid, dim3(64 * kWideWaves), 0, stream, xp, ldx,    \
+                         x_rows, M, row_idx, lp, qp, s, tp, ldt, nbatch);                                      \
       return check_launch("quant_rows_lowrank");                                                               \
     }
     PQ_QWCASE(PQ_BF16, 8) PQ_QWCASE(PQ_BF16, 12) PQ_QWCASE(PQ_BF16, 16) PQ_QWCASE(PQ_BF16, 20) PQ_QWCASE(PQ_BF16, 24)
@@ -935,7 +954,7 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
 #undef PQ_QWCASE
   }
   if (!fused) {
-    const int st = pq_quant_rows_packed(x, x_dtype, M, K, ldx, row_idx, qp, s, stream);
+    const int st = pq_quant_rows_packed(x, x_dtype, M, K, ldx, x_rows, row_idx, qp, s, stream);
     if (st != PQ_OK) return st;
     return pq_lowrank_down(x, x_dtype, M, K, ldx, x_rows, row_idx, l1t, R, t, ldt, stream);
   }

@@ -72,7 +72,8 @@ def _row_index(idx: Optional[torch.Tensor], device) -> Optional[torch.Tensor]:
 def quant_rows(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """x2 [rows, K] bf16/fp16 -> (int8 [M, K], fp32 scale [M]), per-row symmetric absmax
     (deploy/int8_exec.py:216-230). Row-slice views pass without a copy (the kernel takes the row stride).
-    ``row_idx`` (int32 [M]): fused routed gather, output row m quantizes x2[row_idx[m]]."""
+    ``row_idx`` (int32 [M]): fused routed gather, output row m quantizes x2[row_idx[m]]; an entry outside
+    [0, rows) quantizes a row of zeros (codes 0, scale fl(1e-8)/127) where torch's indexing would raise."""
     assert x2.dim() == 2 and x2.is_cuda
     if x2.stride(1) != 1:
         x2 = x2.contiguous()
@@ -82,7 +83,7 @@ def quant_rows(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) -> Tupl
     q = torch.empty((M, K), dtype=torch.int8, device=x2.device)
     s = torch.empty((M,), dtype=torch.float32, device=x2.device)
     L = _lib.load()
-    _lib.check(L.pq_quant_rows(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), _lib.ptr(ri),
+    _lib.check(L.pq_quant_rows(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), rows, _lib.ptr(ri),
                                _lib.ptr(q), _lib.ptr(s), _lib.stream_of(x2.device)), "quant_rows")
     return q, s
 
@@ -156,8 +157,8 @@ def _gemm(xq: torch.Tensor, s_row: torch.Tensor, w_int8: torch.Tensor, w_scale_k
     L = _lib.load()
     _lib.check(L.pq_int8_gemm(_lib.ptr(xq), xq.stride(0), _lib.ptr(w_int8), w_int8.stride(0), _lib.ptr(s_row),
                               _lib.ptr(w_scale_k), group, _lib.ptr(bias), _lib.ptr(t), ldt, _lib.ptr(l2t), R, lr_code,
-                              _lib.ptr(out), out.stride(0), _lib.dtype_code(out_dtype), _lib.ptr(ori), M, N, K,
-                              _lib.stream_of(xq.device)), "int8_gemm")
+                              _lib.ptr(out), out.stride(0), _lib.dtype_code(out_dtype), _lib.ptr(ori), out.shape[0],
+                              M, N, K, _lib.stream_of(xq.device)), "int8_gemm")
     return out
 
 
@@ -166,7 +167,8 @@ def int8_gemm_fused(xq: torch.Tensor, s_row: torch.Tensor, w_int8: torch.Tensor,
                     out_row_idx: Optional[torch.Tensor] = None) -> torch.Tensor:
     """C = (xq @ w_int8^T) * s_row * w_scale (+bias) -> out_dtype in one kernel (deploy/int8_exec.py:202-212).
     Requires K % 64 == 0 and N % 64 == 0 (the reference asserts N % 256 == 0; N = 640 of SDXL also runs here).
-    ``out``/``out_row_idx``: write row m into out[out_row_idx[m]] (routed scatter; other rows untouched)."""
+    ``out``/``out_row_idx``: write row m into out[out_row_idx[m]] (routed scatter; other rows untouched, and a row
+    whose index lies outside [0, out.shape[0]) is not written)."""
     assert xq.shape[1] % 64 == 0 and w_int8.shape[0] % 64 == 0, (xq.shape[1], w_int8.shape[0])
     return _gemm(xq, s_row, w_int8, w_scale, 0, bias, None, None, out_dtype, out, out_row_idx)
 
@@ -228,7 +230,7 @@ def pack_k64(w_int8: torch.Tensor) -> torch.Tensor:
 
 def quant_rows_packed(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """quant_rows with the codes written in the packed K64 layout (flat int8 [packed_rows(M) * K]) for
-    int8_gemm_packed; scales as quant_rows. K % 64 == 0."""
+    int8_gemm_packed; scales and the gather's range rule as quant_rows. K % 64 == 0."""
     assert x2.dim() == 2 and x2.is_cuda
     if x2.stride(1) != 1:
         x2 = x2.contiguous()
@@ -238,8 +240,9 @@ def quant_rows_packed(x2: torch.Tensor, row_idx: Optional[torch.Tensor] = None) 
     q = torch.empty((packed_rows(M) * K,), dtype=torch.int8, device=x2.device)
     s = torch.empty((M,), dtype=torch.float32, device=x2.device)
     L = _lib.load()
-    _lib.check(L.pq_quant_rows_packed(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), _lib.ptr(ri),
-                                      _lib.ptr(q), _lib.ptr(s), _lib.stream_of(x2.device)), "quant_rows_packed")
+    _lib.check(L.pq_quant_rows_packed(_lib.ptr(x2), _lib.dtype_code(x2.dtype), M, K, x2.stride(0), rows,
+                                      _lib.ptr(ri), _lib.ptr(q), _lib.ptr(s), _lib.stream_of(x2.device)),
+               "quant_rows_packed")
     return q, s
 
 
@@ -308,7 +311,7 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
     if out_dtype == torch.int32:
         c = torch.empty((M, N), dtype=torch.int32, device=xq_p.device)
         _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), None, None, 0, None, None, 0, None, 0, 0,
-                                         _lib.ptr(c), N, _lib.PQ_I32, None, M, N, K, _lib.stream_of(xq_p.device)),
+                                         _lib.ptr(c), N, _lib.PQ_I32, None, 0, M, N, K, _lib.stream_of(xq_p.device)),
                    "int8_gemm_packed")
         return c
     assert s_row.dtype == torch.float32 and s_row.is_contiguous() and s_row.numel() >= M
@@ -335,7 +338,7 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
     out_code = _lib.dtype_code(out_dtype) | (_lib.PQ_ACCUMULATE if accumulate else 0)
     _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), _lib.ptr(s_row), _lib.ptr(w_scale), group,
                                      _lib.ptr(bias), _lib.ptr(t), ldt, _lib.ptr(l2t), R, lr_code, _lib.ptr(out),
-                                     out.stride(0), out_code, _lib.ptr(ori), M, N, K,
+                                     out.stride(0), out_code, _lib.ptr(ori), out.shape[0], M, N, K,
                                      _lib.stream_of(xq_p.device)), "int8_gemm_packed")
     return out
 
@@ -536,8 +539,10 @@ class Int8Linear(nn.Module):
                 out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None,
                 accumulate: bool = False) -> torch.Tensor:
         """y = Linear(x) through quantizer (+ low-rank down) + fused GEMM (deploy/int8_exec.py:382-408).
-        Routed use: ``row_idx`` gathers rows of x (2-D x only), ``out``/``out_row_idx`` scatter into a canvas; their
-        entries must be in range (rows of x, rows of out), which the kernels do not check.
+        Routed use: ``row_idx`` gathers rows of x (2-D x only), ``out``/``out_row_idx`` scatter into a canvas. Indices
+        belong in range (rows of x, rows of out). On the kernel paths one that is not never reaches memory past the
+        tensor: a gathered row outside x reads as zeros and a scattered row outside out is not written. The torch
+        fallbacks (low-rank branches above rank 64) index with torch's own ops, which stop the process on it.
         ``accumulate=True`` adds the result into ``out`` (2-D, [rows, N]) instead of overwriting it, each element
         rounded as torch's 16-bit ``out + y`` rounds it: a Linear split along its input sums its halves this way."""
         if accumulate:

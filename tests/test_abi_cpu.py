@@ -49,24 +49,30 @@ def test_invalid_arguments_rejected_without_gpu(lib):
 
     nul = None
     # quantizer: null pointers, bad shapes, bad dtype
-    assert lib.pq_quant_rows(nul, 0, 4, 64, 64, nul, nul, nul, nul) == L.PQ_EINVAL
-    assert lib.pq_quant_rows(nul, 0, -1, 64, 64, nul, nul, nul, nul) == L.PQ_ESHAPE
-    assert lib.pq_quant_rows(ctypes.c_void_p(16), 0, 4, 64, 32, nul, ctypes.c_void_p(16), ctypes.c_void_p(16),
+    assert lib.pq_quant_rows(nul, 0, 4, 64, 64, 4, nul, nul, nul, nul) == L.PQ_EINVAL
+    assert lib.pq_quant_rows(nul, 0, -1, 64, 64, 4, nul, nul, nul, nul) == L.PQ_ESHAPE
+    assert lib.pq_quant_rows(ctypes.c_void_p(16), 0, 4, 64, 32, 4, nul, ctypes.c_void_p(16), ctypes.c_void_p(16),
                              nul) == L.PQ_ESHAPE          # ldx < K
-    assert lib.pq_quant_rows(ctypes.c_void_p(16), 7, 4, 64, 64, nul, ctypes.c_void_p(16), ctypes.c_void_p(16),
+    assert lib.pq_quant_rows(ctypes.c_void_p(16), 7, 4, 64, 64, 4, nul, ctypes.c_void_p(16), ctypes.c_void_p(16),
                              nul) == L.PQ_EDTYPE
-    assert lib.pq_quant_rows(nul, 0, 0, 64, 64, nul, nul, nul, nul) == L.PQ_OK      # empty: nothing to do
+    assert lib.pq_quant_rows(nul, 0, 0, 64, 64, 0, nul, nul, nul, nul) == L.PQ_OK      # empty: nothing to do
+    # x_rows: at least one row, and every row of an ungathered x
+    assert lib.pq_quant_rows(ctypes.c_void_p(16), 0, 4, 64, 64, 3, nul, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                             nul) == L.PQ_ESHAPE
+    assert b"x_rows" in lib.pq_last_error()
+    assert lib.pq_quant_rows_packed(ctypes.c_void_p(16), 0, 4, 64, 64, 0, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                    ctypes.c_void_p(16), nul) == L.PQ_ESHAPE
     assert b"dtype" in lib.pq_last_error() or lib.pq_last_error() is not None
     # GEMM: K % 64, N % 64, alignment, group, rank
     p16 = ctypes.c_void_p(256)
     args = dict(a=p16, lda=128, w=p16, ldw=128, s_row=p16, s_w=p16, group=0, bias=nul, t=nul, ldt=0, l2t=nul, R=0,
-                lr=0, c=p16, ldc=128, od=0, ori=nul, M=8, N=128, K=128, st=nul)
+                lr=0, c=p16, ldc=128, od=0, ori=nul, c_rows=0, M=8, N=128, K=128, st=nul)
 
     def gemm(**kw):
         a = dict(args, **kw)
         return lib.pq_int8_gemm(a["a"], a["lda"], a["w"], a["ldw"], a["s_row"], a["s_w"], a["group"], a["bias"],
                                 a["t"], a["ldt"], a["l2t"], a["R"], a["lr"], a["c"], a["ldc"], a["od"], a["ori"],
-                                a["M"], a["N"], a["K"], a["st"])
+                                a["c_rows"], a["M"], a["N"], a["K"], a["st"])
 
     assert gemm(K=96, lda=96, ldw=96) == L.PQ_ESHAPE
     assert gemm(N=96) == L.PQ_ESHAPE
@@ -78,7 +84,12 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert gemm(t=p16, l2t=p16, R=24, ldt=24) == L.PQ_ESHAPE
     assert gemm(t=p16, l2t=nul, R=32, ldt=32) == L.PQ_EINVAL
     assert gemm(t=p16, l2t=p16, R=32, ldt=(1 << 22) + 8) == L.PQ_ESHAPE   # t rows at 32-bit buffer offsets
-    assert lib.pq_int8_gemm_packed(p16, p16, p16, p16, 0, nul, p16, (1 << 22) + 8, p16, 32, 0, p16, 128, 0, nul,
+    assert lib.pq_int8_gemm_packed(p16, p16, p16, p16, 0, nul, p16, (1 << 22) + 8, p16, 32, 0, p16, 128, 0, nul, 0,
+                                   8, 128, 128, nul) == L.PQ_ESHAPE
+    # a scatter needs the canvas's row count
+    assert gemm(ori=p16, c_rows=0) == L.PQ_ESHAPE
+    assert b"c_rows" in lib.pq_last_error()
+    assert lib.pq_int8_gemm_packed(p16, p16, p16, p16, 0, nul, nul, 0, nul, 0, 0, p16, 128, 0, p16, 0,
                                    8, 128, 128, nul) == L.PQ_ESHAPE
     assert gemm(od=5) == L.PQ_EDTYPE or gemm(od=5) == L.PQ_ELAUNCH
     assert gemm(M=0) == L.PQ_OK
@@ -88,7 +99,7 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, 8, nul, p16, 24, p16, 32, nul) == L.PQ_ESHAPE
     assert lib.pq_lowrank_down(p16, 0, 8, 128, 128, 4, nul, p16, 32, p16, 32, nul) == L.PQ_ESHAPE   # x_rows < M
     # grids beyond the 32-bit work-item count of one dispatch are refused before any launch
-    assert lib.pq_quant_rows(p16, 0, (1 << 26) + 64, 64, 64, nul, p16, p16, nul) == L.PQ_ESHAPE
+    assert lib.pq_quant_rows(p16, 0, (1 << 26) + 64, 64, 64, (1 << 26) + 64, nul, p16, p16, nul) == L.PQ_ESHAPE
     assert b"32-bit dispatch" in lib.pq_last_error()
     assert lib.pq_pack_k64(p16, 1 << 31, 64 * 1024, 64 * 1024, p16, nul) == L.PQ_ESHAPE
     assert lib.pq_int8_gemm_i32(p16, 64, p16, 64, p16, 1 << 16, 1 << 30, 1 << 16, 64, nul) == L.PQ_ESHAPE
