@@ -760,9 +760,15 @@ int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
   if constexpr (MODE == kModeGroup32) {
     // fp32 accumulators live in VGPRs (the VALU rescales them every group): 128 x 128 blocks, two per CU; with
     // fewer than 512 of them, 128 x 64 blocks (the VALU-bound kernel then spreads over twice the CUs: measured
-    // 1.2-1.5x faster at M = 2048 for the SDXL shapes, slower once the 128 x 128 blocks fill the chip)
-    if (small_blocks(a) < 512) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
-    return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
+    // 1.2-1.5x faster at M = 2048 for the SDXL shapes, slower once the 128 x 128 blocks fill the chip). With a
+    // low-rank epilogue always 128 x 64: at 128 x 128 its slices of t and l2t push the kernel past its 256 VGPRs
+    // (5-49 spilled).
+    if constexpr (LRS > 0) {
+      return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
+    } else {
+      if (small_blocks(a) < 512) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
+      return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
+    }
   } else {
     if (big_tiles(a)) return launch_dma<4, 2, 4, 1, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
     // fewer 128 x 128 blocks than half the CUs: 128 x 64 blocks (measured 1.3x faster at 80 blocks, even at 160)

@@ -682,9 +682,13 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
   for (int rho = 0; rho < 2; ++rho)
     qlane[rho] = (lane >> 3) * 1024 + ((((lane >> 1) & 3) ^ k64_swz(2 * wave + rho)) << 4) + (lane & 1) * 8;
   v4u v[2][NCH];
+  // live[rho]: row rho of the batch in hand has a source row (decided when its loads were issued, one batch ahead:
+  // recomputing it per batch cost the K = 12288 kernel a spilled register)
+  bool live[2] = {false, false};
   if (blockIdx.x < nbatch) {
 #pragma unroll
     for (int rho = 0; rho < 2; ++rho) {
+      live[rho] = src_of(blockIdx.x, rho) >= 0;
       const v4u* xr = src_row(blockIdx.x, rho);
 #pragma unroll
       for (int c = 0; c < NCH; ++c) v[rho][c] = __builtin_nontemporal_load(xr + c * 64 + lane);
@@ -698,10 +702,11 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
     for (int rho = 0; rho < 2; ++rho) {
       mrow[rho] = (int64_t)b * 16 + 2 * wave + rho;
       xn[rho] = src_row(bn < nbatch ? bn : b, rho);
-      if (src_of(b, rho) < 0) {   // a padding row or a gathered row outside x: it quantizes as zeros
+      if (!live[rho]) {   // a padding row or a gathered row outside x: it quantizes as zeros
 #pragma unroll
         for (int c = 0; c < NCH; ++c) v[rho][c] = v4u{0u, 0u, 0u, 0u};
       }
+      live[rho] = src_of(bn < nbatch ? bn : b, rho) >= 0;   // the batch whose loads xn starts
     }
     dma_l(0);   // lands before slab 0's barrier: only that slab's code stores and next-batch loads come after it
     float sc[2], rc[2];
