@@ -200,6 +200,12 @@ struct Epilogue {
     const int* orows = reinterpret_cast<const int*>(rbuf + 1024);
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
+      v4f srt[4];   // transposed tiles: s_row of this lane's 16 rows of tile j
+      if constexpr (kT) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          srt[q] = *reinterpret_cast<const v4f*>(rbuf + (mloc + j * 32 + 8 * q + 4 * khalf) * 4);
+      }
 #pragma unroll
       for (int ih = 0; ih < TI / 2; ++ih) {
         // staging -> global: 8 lanes x 16 bytes per 128-byte row piece, 8 rows per store instruction
@@ -229,6 +235,11 @@ struct Epilogue {
         for (int ii = 0; ii < 2; ++ii) {
           const int i = 2 * ih + ii;
           const int nl = nloc + 32 * i;
+          if constexpr (kT) {
+            const float bn = has_bias ? reinterpret_cast<const float*>(cbuf + 1024)[nl + (lane & 31)] : 0.0f;
+            tile_t(acc[i][j], srt, bn, has_bias, stage + 4 * khalf * kPitchL + (ii * 32 + (lane & 31)) * 2, kPitchL);
+            continue;
+          }
           if constexpr (MODE == kModeChannel) {
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -294,6 +305,28 @@ struct Epilogue {
           v2u{pack2<ODT>(y[4 * q + 0], y[4 * q + 1]), pack2<ODT>(y[4 * q + 2], y[4 * q + 3])};
   }
 
+  // Group-32 without a low-rank term keeps its tiles transposed (see the main loop): lane l holds output column
+  // n = l % 32 and rows 8 (r / 4) + 4 (l / 32) + r % 4. Same per-element dequant as tile() (y = acc * s_row[m],
+  // + bias[n]); srt holds the s_row of the lane's 16 rows, bn its column's bias. Each converted pair (rows m, m + 1)
+  // goes to the row-major staging area as two 16-bit writes: `col` is this lane's column in row 4 (l / 32).
+  static constexpr bool kT = MODE == kModeGroup32 && LRS == 0;
+  __device__ __forceinline__ void tile_t(const v16f& a, const v4f (&srt)[4], float bn, bool has_bias, uint8_t* col,
+                                         int pitch) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        float y0 = a[4 * q + e] * srt[q][e], y1 = a[4 * q + e + 1] * srt[q][e + 1];
+        if (has_bias) {
+          y0 = y0 + bn;
+          y1 = y1 + bn;
+        }
+        const uint32_t v = pack2<ODT>(y0, y1);
+        *reinterpret_cast<uint16_t*>(col + (8 * q + e) * pitch) = (uint16_t)(v & 0xffffu);
+        *reinterpret_cast<uint16_t*>(col + (8 * q + e + 1) * pitch) = (uint16_t)(v >> 16);
+      }
+  }
+
   // Rows of the wave's output sub-tile (32 TJ rows of 32 TI outputs) staged in LDS by run(): 16-bit outputs,
   // rows padded by 16 bytes so that the column-wise fragment writes spread over the banks.
   static constexpr int kRowBytes = 64 * TI;
@@ -348,8 +381,23 @@ struct Epilogue {
         const int c = CB == 2 ? (i & 1) : 0;
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-          // fragment -> staging rows: row (32 j + lane % 32), outputs 32 i + 8 q + 4 (lane / 32) .. + 3
-          tile(acc[i][j], j, c, has_bias, stage + (j * 32 + (lane & 31)) * kPitch + (i * 32 + 4 * khalf) * 2);
+          if constexpr (kT) {
+            // transposed tile: the lane's column n and its 16 rows (s_row clamped at the last row: rows past M are
+            // computed but not stored)
+            const int m0 = mbase + j * 32 + 4 * khalf;
+            v4f srt[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) srt[q][e] = p.s_row[min(m0 + 8 * q + e, p.M - 1)];
+            const int n = nbase + i * 32 + (lane & 31);
+            const float bn = has_bias && n < p.N ? p.bias[n] : 0.0f;
+            tile_t(acc[i][j], srt, bn, has_bias, stage + (j * 32 + 4 * khalf) * kPitch + (i * 32 + (lane & 31)) * 2,
+                   kPitch);
+          } else {
+            // fragment -> staging rows: row (32 j + lane % 32), outputs 32 i + 8 q + 4 (lane / 32) .. + 3
+            tile(acc[i][j], j, c, has_bias, stage + (j * 32 + (lane & 31)) * kPitch + (i * 32 + 4 * khalf) * 2);
+          }
           __builtin_amdgcn_sched_barrier(0);   // keep one tile's epilogue live at a time
         }
       }
@@ -601,7 +649,24 @@ void gemm_dma_kernel(const GemmArgs p) {
   // semantics: pyraquant/quantizers_weight.py:96-109). Lane element r of tile i holds row
   // n = wn BN / 2 + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4.
   auto mm = [&](const v4i (&f)[NF], int kt, int s) {
-    if constexpr (G32) {
+    if constexpr (G32 && LRS == 0) {
+      // Transposed tiles (no low-rank term to line up with): the activation fragment is the MFMA's first operand, so
+      // lane l holds output column n = l % 32 of each tile and its 16 rows m; all 16 partials of a lane share one
+      // scale s_w[g, n], one dword per weight tile and group instead of the 16-value stripe of the other layout.
+      const float* sgt =
+          reinterpret_cast<const float*>(sscale + (kt % SLOTS) * SB) + s * BN + wn * (BN / 2) + (lane & 31);
+      float sv[TI];
+#pragma unroll
+      for (int i = 0; i < TI; ++i) sv[i] = sgt[i * 32];
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          const v16i part = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[TI + j], f[i], v16i{}, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(sv[i], (float)part[r], acc[i][j][r]);
+        }
+    } else if constexpr (G32) {
       const float* sg = reinterpret_cast<const float*>(sscale + (kt % SLOTS) * SB) + s * BN + wn * (BN / 2) + 4 * kh;
 #pragma unroll
       for (int i = 0; i < TI; ++i) {
