@@ -1,4 +1,4 @@
-"""The reference's torch CPU quantize + int-matmul path, restated -- TEST / BASELINE INFRASTRUCTURE ONLY.
+"""The reference's torch CPU quantize + int-matmul path, restated -- TEST AND CPU-BASELINE INFRASTRUCTURE ONLY.
 
 Used only as bench.py's ``cpu_baseline`` leg (kind "port") and as an independent cross-check of the C oracle in
 tests/. Never imported by the product package.

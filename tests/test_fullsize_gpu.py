@@ -1,5 +1,5 @@
-"""Full-size parity: Int8Linear.forward at every BASELINE configuration's real shape, checked against the CPU oracle
-on sampled rows (deploy/int8_exec.py:382-393 for the layer, :303-309 for the epilogue order).
+"""Full-size parity: Int8Linear.forward at every benchmark configuration's real shape (c1, c2a, c2b, c3, c4), checked
+against the CPU oracle on sampled rows (deploy/int8_exec.py:382-393 for the layer, :303-309 for the epilogue order).
 
 Each case runs the whole layer on the GPU (the module's own path: the fused quantizer + low-rank pass or the packed
 quantizer, then the packed GEMM with its epilogue), then takes 64 seeded random rows plus the last 40 rows (the last,
