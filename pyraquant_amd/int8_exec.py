@@ -449,7 +449,9 @@ class Int8Linear(nn.Module):
                 At = A.new_zeros((r_down, K))
                 At[:R] = A.t()
             self.register_buffer("lr_At", At)
-            self.register_buffer("lr_At_frag", None if At is None else pack_lowrank_l1t(At), persistent=False)
+            self.register_buffer("lr_At_frag", None, persistent=False)
+            self._lr_frag_key = None
+            self._lr_frag()
             Bt = B.new_zeros((N, r_epi)) if r_epi else None
             if Bt is not None:
                 Bt[:, :R] = B.t()
@@ -459,6 +461,7 @@ class Int8Linear(nn.Module):
             self.lr_B = None
             self.lr_At = None
             self.lr_At_frag = None
+            self._lr_frag_key = None
             self.lr_Bt = None
         del w
 
@@ -478,11 +481,17 @@ class Int8Linear(nn.Module):
         return self
 
     def _lr_frag(self) -> Optional[torch.Tensor]:
-        """lr_At_frag where it still matches lr_At (a module-wide cast or move carries both the same way)."""
-        f = self.lr_At_frag
-        if f is None or self.lr_At is None or f.dtype != self.lr_At.dtype or f.device != self.lr_At.device:
+        """lr_At in fragment order, repacked whenever lr_At is not the tensor it was packed from: a module-wide cast
+        or move, load_state_dict (which copies into lr_At in place) or any other in-place update (torch's version
+        counter). None where no fragment order exists for lr_At's shape."""
+        At = self.lr_At
+        if At is None:
             return None
-        return f
+        key = (At.data_ptr(), At._version, At.dtype, At.device)
+        if key != self._lr_frag_key:
+            self.lr_At_frag = pack_lowrank_l1t(At) if At.is_cuda and At.is_contiguous() else None
+            self._lr_frag_key = key
+        return self.lr_At_frag
 
     def _scale_k(self) -> torch.Tensor:
         return self.w_scale_gn if self.group_size else self.w_scale

@@ -205,3 +205,25 @@ def test_int8linear_keeps_fragment_order_through_casts(cuda):
     yh = q(xh)
     q.lr_At_frag = None
     assert torch.equal(yh.view(torch.int16), q(xh).view(torch.int16))
+
+
+def test_int8linear_fragment_order_follows_lr_At(cuda):
+    """lr_At_frag is derived from lr_At: after load_state_dict (an in-place copy into lr_At) or an in-place edit of
+    lr_At the module repacks it, so the one-pass kernel never reads a stale copy. Checked against a module built from
+    the loaded weights and against the row-major path after the edit."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    q1 = E.Int8Linear(make_linear(3072, 640, 32, True, seed=5), device=cuda)
+    q2 = E.Int8Linear(make_linear(3072, 640, 32, True, seed=6), device=cuda)
+    x = make_x(333, 3072, torch.bfloat16, seed=9, device=cuda)
+    y2 = q2(x)
+    q1.load_state_dict(q2.state_dict())
+    assert torch.equal(q1(x).view(torch.int16), y2.view(torch.int16))
+    with torch.no_grad():
+        q1.lr_At.mul_(2)
+    y_frag = q1(x)                   # repacked from the edited lr_At
+    q1.lr_At_frag = None             # the row-major path, same lr_At
+    y_plain = q1(x)
+    assert torch.equal(y_frag.view(torch.int16), y_plain.view(torch.int16))
+    assert not torch.equal(y_frag.view(torch.int16), y2.view(torch.int16))
