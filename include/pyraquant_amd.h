@@ -129,6 +129,12 @@ int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t 
  * c 8-byte aligned with ldc % 4 == 0 and ldc < 2^31; t, l2t 16-byte aligned with ldt % 8 == 0, ldt <= 2^22,
  * R in {16, 32, 64}; group 32 needs N * K < 2^33 (its scales are read at 32-bit buffer offsets);
  * lr_dtype and out_dtype are PQ_BF16 or PQ_F16; out_row_idx entries unique (two rows naming one row of c race).
+ * Large products (rank 0-32, no accumulate, more 256 x 256 blocks than CUs) run one persistent workgroup per CU
+ * that claims blocks from per-XCD counters in a 36-byte device buffer belonging to the calling thread's device and
+ * the stream: the library allocates it on the first such launch on that stream (never while the stream is being
+ * captured, and in relaxed capture mode), and each launch leaves it zeroed for the next. Launches on different
+ * streams never share one. A stream being captured gets a fixed share of blocks per workgroup instead, as does
+ * pq_int8_linear_noalloc, so a graph replays without the buffer. The results do not depend on the schedule.
  */
 int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
                  const float* s_row, const float* s_w, int64_t group, const float* bias,
@@ -177,7 +183,8 @@ int pq_pack_lowrank_l1t(const void* l1t, int32_t dtype, int64_t R, int64_t K, vo
  * output, group 0), each output element is added to what c holds: c = round(c + round(y)), so a Linear split along
  * its input accumulates its second half into the first half's output in the same pass that writes it
  * (`SplitInLinear.forward`'s `L0(x0) + L1(x1)`, pyraquant/external_quant.py:191-192). This is the layer path of Int8Linear: the quantizer writes ap directly
- * (pq_quant_rows_packed) and the weights are packed once at conversion (pq_pack_k64).
+ * (pq_quant_rows_packed) and the weights are packed once at conversion (pq_pack_k64). Large products run persistent
+ * workgroups with the stream's scheduling buffer, as pq_int8_gemm describes.
  * Replaces `int8_gemm_fused` / `int8_gemm_lr` (deploy/int8_exec.py:202-212, 327-336) as called from
  * `Int8Linear.forward` (deploy/int8_exec.py:382-393).
  */
@@ -202,7 +209,8 @@ int64_t pq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t R);
  * weights [N, K]; s_w [N] (group 0) or [K/32, N] (group 32); bias [N] fp32 or NULL; l1t [R, K] and l2t [N, Re] in
  * x's dtype (R a multiple of 32 up to 128, Re in {16, 32, 64} and Re <= R: the first Re columns of t enter the
  * epilogue), or NULL with R = Re = 0; l1f NULL or l1t in fragment order (as pq_quant_rows_lowrank); y [M, N] in
- * x's dtype with row stride ldy. Same results as the two calls.
+ * x's dtype with row stride ldy. Same results as the two calls. Its GEMM uses the stream's scheduling buffer as
+ * pq_int8_gemm describes (allocated once per stream, outside the workspace).
  * Replaces the body of `Int8Linear.forward` (deploy/int8_exec.py:382-393): one C call per layer.
  */
 int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,

@@ -15,6 +15,13 @@ int check_launch(const char* what);
 // A dispatch counts work-items in 32 bits per dimension: blocks * threads must stay below 2^32.
 int check_grid(int64_t blocks, int64_t threads, const char* what);
 
+// pq_int8_gemm_packed with the choice of whether a large GEMM may allocate its stream's scheduling buffer
+// (pq_gemm.hip); the allocation-free layer call passes false.
+int int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w, int64_t group,
+                     const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
+                     void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows, int64_t M,
+                     int64_t N, int64_t K, hipStream_t stream, bool sched_alloc);
+
 // ---- vector types of the MFMA operands -----------------------------------------------------------------
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));

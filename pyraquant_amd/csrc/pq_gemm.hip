@@ -30,10 +30,14 @@
 // VALU-bound at a quarter of the INT8 MFMA rate; blocks are 128 x 128 at two workgroups per CU.
 //
 // Workgroup ids are remapped so that each XCD (ids are dealt round-robin over the 8 XCDs) walks a contiguous
-// run of tiles, rasterised in groups of group_m() m-tiles for L2 reuse.
+// run of tiles, rasterised in groups of group_m() m-tiles for L2 reuse. Large 256 x 256 products run one persistent
+// workgroup per CU, which claims its XCD's tiles (then the other XCDs') through a per-stream scheduling buffer.
 #include "pq_common.h"
 
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
 
 namespace pq {
 namespace {
@@ -58,6 +62,8 @@ struct GemmArgs {
   int64_t lda, ldw, ldt, ldc;
   int M, N, K, R;
   int tiles_m, tiles_n;
+  int* sched;         // persistent blocks: 9 ints of claim counters, zero at launch and left zero (or NULL)
+  bool sched_alloc;   // host side: the entry may allocate a scheduling buffer for the stream (not noalloc)
 };
 
 enum { kModeI32 = 0, kModeChannel = 1, kModeGroup32 = 2 };
@@ -454,6 +460,26 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// Whether the block's epilogue takes its operands through the ring (run_lds): the row and column slots must fit one
+// stage each and the operand DMA slots of one stage, and the output staging the remaining NS - 2 buffers.
+template <int TI, int TJ, int WMW, int NS, int OCC, int MODE, int LRS, int LRDT, int ODT, bool ACC>
+constexpr bool epilogue_in_ring() {
+  using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT, OCC * WMW == 2 ? 2 : 1, OCC == 1, ACC>;
+  constexpr int NW = 2 * WMW, BN = 64 * TI, BM = 32 * TJ * WMW;
+  constexpr int stage = (BN + BM) * kBKd, dma = (BN + BM) / 16;   // bytes and 1 KB DMA slots of a stage
+  constexpr int lr = LRS * 16 * 2;                                // one low-rank row
+  constexpr int rows = 2 + BM * lr / 1024, cols = 2 + BN * lr / 1024;
+  return MODE != kModeI32 && TI % 2 == 0 && NS >= 3 && BN <= 256 && BM <= 256 && rows * 1024 <= stage &&
+         cols * 1024 <= stage && rows <= dma && cols <= dma && (NS - 2) * (stage / Epi::kStageBytesL) >= NW;
+}
+
+// Persistent blocks (see the kernel): the 256 x 256 tile at one workgroup per CU with its epilogue operands in the
+// ring and no accumulate (the other variants keep one tile per workgroup: in a loop they spill registers).
+template <int TI, int TJ, int WMW, int NS, int OCC, int MODE, int LRS, int LRDT, int ODT, bool ACC>
+constexpr bool persistent_block() {
+  return OCC == 1 && TI == 4 && WMW == 4 && !ACC && epilogue_in_ring<TI, TJ, WMW, NS, OCC, MODE, LRS, LRDT, ODT, ACC>();
+}
+
 // WMW waves along m (2 or 4) times 2 along n; OCC workgroups per CU.
 template <int TI, int TJ, int WMW, int NS, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT, bool ACC = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(128 * WMW, 128 * WMW),
@@ -473,15 +499,11 @@ void gemm_dma_kernel(const GemmArgs p) {
   constexpr int DS = SB / 256 / NW;           // 256-byte (dword) DMA instructions per wave and stage (scales)
   static_assert(DW * 16 * NW == BN && DA * 16 * NW == BM && DS * 256 * NW == SB, "DMA split over the waves");
   constexpr int DPW = DW + DA + DS;
-  // Epilogue operands through the ring (run_lds): the row and column slots must fit one stage each and the
-  // operand DMA slots of one stage, and the output staging the remaining NS - 2 buffers.
+  // Epilogue operands through the ring (run_lds): see epilogue_in_ring.
   using Epi = Epilogue<TI, TJ, MODE, LRS, LRDT, ODT, OCC * WMW == 2 ? 2 : 1, OCC == 1, ACC>;
   constexpr int kLrBytes = LRS * 16 * 2;                       // one low-rank row
   constexpr int kRowSlots = 2 + BM * kLrBytes / 1024, kColSlots = 2 + BN * kLrBytes / 1024;
-  constexpr bool ELDS = MODE != kModeI32 && TI % 2 == 0 && NS >= 3 && BN <= 256 && BM <= 256 &&
-                        kRowSlots * 1024 <= WB + AB && kColSlots * 1024 <= WB + AB &&
-                        kRowSlots <= NW * (DW + DA) && kColSlots <= NW * (DW + DA) &&
-                        (NS - 2) * ((WB + AB) / Epi::kStageBytesL) >= NW;
+  constexpr bool ELDS = epilogue_in_ring<TI, TJ, WMW, NS, OCC, MODE, LRS, LRDT, ODT, ACC>();
   constexpr int NF = TI + TJ;                 // fragments per substep
   constexpr int kRest = TI * TJ - NF;         // MFMAs of a substep beyond the NF that carry a fragment read
   constexpr int kVPer = kRest > 0 ? (DPW + kRest - 1) / (kRest > 0 ? kRest : 1) : 0;   // DMA per such MFMA
@@ -495,8 +517,32 @@ void gemm_dma_kernel(const GemmArgs p) {
   const int wn = wave & 1;
   const int wm = wave >> 1;
 
+  // Persistent blocks (the 256 x 256 tile with its epilogue operands in the ring, no accumulate): one workgroup per
+  // CU loops over tiles, which takes the relaunch gap out of every tile after the first. Virtual block vb is the id
+  // the launch-per-tile grid would have given the tile (tile_coords: XCD vb % 8, its local index vb / 8), so a
+  // workgroup stays on its XCD's tiles and the raster is unchanged. The first tile of workgroup b is vb = b. After
+  // that, with a scheduling buffer (p.sched: 8 per-XCD claim counters and an exit count, zero at launch), a
+  // workgroup claims the next local index of its own XCD's tiles, and once those are gone it claims from the other
+  // XCDs' lists. The XCDs of one chip run the loop at different speeds (up to 5 % apart), so fixed shares finish
+  // up to 165 us apart at c1. Without the buffer it steps vb by the grid size (a fixed share per workgroup).
+  constexpr bool PERSIST = persistent_block<TI, TJ, WMW, NS, OCC, MODE, LRS, LRDT, ODT, ACC>();
+  const int nbt = p.tiles_m * p.tiles_n;
+  auto claim = [&](int vb) -> int {   // the virtual block after vb
+    if (!p.sched) return vb + (int)gridDim.x;
+    const int per = nbt >> 3, rem = nbt & 7, x0 = blockIdx.x & 7, rot = blockIdx.x >> 3;
+    for (int k = 0; k < 8; ++k) {
+      const int x = k == 0 ? x0 : (x0 + 1 + (k - 1 + rot) % 7) & 7;   // own list, then the other 7 in turn
+      const int cnt = per + (x < rem ? 1 : 0);                        // XCD x's tiles
+      const int first = ((int)gridDim.x - x + 7) >> 3;                // of them taken as first tiles
+      if (first >= cnt) continue;
+      const int li = atomicAdd(p.sched + x, 1) + first;
+      if (li < cnt) return (li << 3) | x;
+    }
+    return nbt;
+  };
+  for (int vb = blockIdx.x; vb < nbt;) {
   int tm, tn;
-  tile_coords<group_m<OCC>()>(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+  tile_coords<group_m<OCC>()>(vb, nbt, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * BM;
   const int n0 = tn * BN;
 
@@ -593,18 +639,22 @@ void gemm_dma_kernel(const GemmArgs p) {
         const int lrec = LRS ? (int)((rows_x - 1) * lrs * 2 + kLrBytes) : 0;
         const __amdgpu_buffer_rsrc_t rs_l = __builtin_amdgcn_make_buffer_rsrc(
             LRS ? (void*)lp : (void*)p.s_w, (short)0, lrec, kBufferWord3);
+        // The slot offsets come from a lane number the compiler cannot see through, so they are computed at each
+        // call: in the persistent loop it would otherwise keep them for every tile (17 64-bit values, spilled).
+        int lane_t = lane;
+        asm volatile("" : "+v"(lane_t));
 #pragma unroll
         for (int i = 0; i < DW + DA; ++i) {
           const int qd = wave * (DW + DA) + i;   // destination slot (distinct for every instruction of the WG)
           const int q = min(qd, nsl - 1);        // source chunk
-          int vo = lane * 16;
+          int vo = lane_t * 16;
           __amdgpu_buffer_rsrc_t rs = q == 0 ? rs_v : rs_i;
           if (q >= 2) {
             // packed byte of slot lane: line L = 16 (q - 2) + lane / 4, stored chunk (lane % 4) ^ swz(L % 16)
-            const int pb = ((q - 2) * 16 + (lane >> 2)) * 64 + (((lane & 3) ^ swz(lane >> 2)) << 4);
+            const int pb = ((q - 2) * 16 + (lane_t >> 2)) * 64 + (((lane_t & 3) ^ swz(lane_t >> 2)) << 4);
             constexpr int kLb = kLrBytes > 0 ? kLrBytes : 1;   // (no low rank: never reached)
             const int row = pb / kLb, cb = pb % kLb;
-            vo = (int)(row * lrs * 2) + cb;
+            vo = row * (int)lrs * 2 + cb;   // below lrec, a 32-bit value
             rs = rs_l;
           }
           __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)(sb + qd * 1024), 16, vo, 0, 0, 0);
@@ -719,18 +769,18 @@ void gemm_dma_kernel(const GemmArgs p) {
   // Ring: stage s lives in buffer s % NS. The DMA of stage s is issued after the barrier of iteration s - NS and
   // must have landed at the barrier that ends iteration s - 1, NS - 1 iterations later; in between, the DMAs of
   // NS - 2 younger stages may still be in flight, hence vmcnt((NS - 2) * DPW).
-  // Prologue: stage 0 alone before the first barrier (the barrier's release fence waits for every LDS-DMA this
-  // wave has in flight), stages 1 .. NS - 1 right after the first fragment reads.
-  if (KT > 0) dma(0, 0);
-  else dma_tail(0, 0);
-  wait_dma<0>();
-  __syncthreads();
-  rd(f0, 0, 0);
+  // Prologue: all NS stages go out at once; the first barrier waits for stage 0 only (the explicit barrier: a
+  // fenced one would wait for every DMA in flight). Issuing stages 1 .. NS - 1 only after stage 0 had landed put a
+  // second memory latency in front of every tile.
 #pragma unroll
-  for (int st = 1; st < NS; ++st) {
+  for (int st = 0; st < NS; ++st) {
     if (st < KT) dma(st, st);
     else dma_tail(st, st);
   }
+  wait_dma<(NS - 1) * DPW>();   // this wave's stage 0 has landed
+  lds_barrier();                // every wave's has
+  __builtin_amdgcn_sched_barrier(0);
+  rd(f0, 0, 0);
   auto iter = [&](int kt, int b, int bn, auto tail) {
     rd(f1, b, 1);
     mm(f0, kt, 0);
@@ -765,6 +815,9 @@ void gemm_dma_kernel(const GemmArgs p) {
   mm(f1, KT - 1, 1);
   wait_dma<0>();     // the epilogue operands, and the out-of-range DMAs of the last iterations, have landed
   __syncthreads();   // every wave is done reading the ring: it becomes the output staging area
+  // the next tile's claim goes out now and is used after the epilogue, which covers its latency
+  int next = nbt;
+  if (PERSIST && wave == 0 && lane == 0) next = claim(vb);
   if constexpr (ELDS) {
     // buffers of stages KT (rows) and KT + 1 (columns) hold the operands; staging in the NS - 2 others
     constexpr int kSpb = STAGE / Epi::kStageBytesL;
@@ -775,6 +828,27 @@ void gemm_dma_kernel(const GemmArgs p) {
   } else {
     static_assert(ELDS || NW * Epi::kStageBytes <= NS * STAGE, "output staging must fit the LDS ring");
     epi.run(p, acc, nbase, mbase, lane, smem + wave * Epi::kStageBytes);
+  }
+  if constexpr (PERSIST) {
+    // The next tile reaches every wave through the last 4 bytes of the row-operand buffer: its last DMA slot is
+    // past the row operands (kRowSlots < 32), so the epilogue never reads it, and the next tile's DMA overwrites it
+    // only after the second barrier.
+    static_assert(kRowSlots < NW * (DW + DA), "the row buffer's last slot holds no epilogue operand");
+    int* const slot = reinterpret_cast<int*>(smem + (KT % NS) * STAGE + STAGE - 4);
+    if (wave == 0 && lane == 0) *slot = next;
+    lds_barrier();
+    vb = *slot;
+    lds_barrier();   // every wave has read it, and is done with the staging area, before the next tile's DMA
+  } else {
+    vb = nbt;
+  }
+  }
+  // The last workgroup out leaves the scheduling buffer as it found it (zero) for the next launch on its stream.
+  if (PERSIST && p.sched && wave == 0 && lane == 0) {
+    if (atomicAdd(p.sched + 8, 1) == (int)gridDim.x - 1) {
+#pragma unroll
+      for (int x = 0; x < 9; ++x) atomicExch(p.sched + x, 0);
+    }
   }
 }
 
@@ -797,12 +871,84 @@ constexpr int ring_stages() {
   return ns < 8 ? ns : 8;
 }
 
+// Compute units of the current device, rounded down to a multiple of the 8 XCDs (a persistent grid keeps workgroup
+// b on XCD b % 8); 0 if unknown.
+int persistent_workgroups() {
+  static int cached[64];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  cus &= ~7;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
+}
+
+// The scheduling buffer of a stream: 9 ints on the stream's device, zeroed once when first handed out (in the
+// stream's order) and left zero by every launch that uses it, so launches on one stream share it and launches on
+// different streams never do. NULL while the stream is being captured (a graph keeps the static schedule, so a
+// replay never shares a buffer with eager launches) or if the allocation fails. The allocation runs in relaxed
+// capture mode so that another thread's global-mode capture is not invalidated by it. At most 1024 buffers per
+// process; later streams get NULL.
+int* stream_sched(hipStream_t stream) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (cs != hipStreamCaptureStatusNone) return nullptr;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, int*> bufs;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(dev, stream);
+  const auto it = bufs.find(key);
+  if (it != bufs.end()) return it->second;
+  if (bufs.size() >= 1024) return nullptr;
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  int* buf = nullptr;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&buf), 9 * sizeof(int));
+  if (e == hipSuccess) e = hipMemsetAsync(buf, 0, 9 * sizeof(int), stream);
+  (void)hipThreadExchangeStreamCaptureMode(&mode);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    if (buf) (void)hipFree(buf);
+    return nullptr;
+  }
+  bufs.emplace(key, buf);
+  return buf;
+}
+
 template <int TI, int TJ, int WMW, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT, bool ACC = false>
 int launch_dma(GemmArgs& a, hipStream_t stream) {
   constexpr int NS = ring_stages<TI, TJ, WMW, OCC, MODE>();
   dim3 grid;
   const int st = grid_of(a, 32 * TJ * WMW, 64 * TI, 128 * WMW, grid);
   if (st != PQ_OK) return st;
+  a.sched = nullptr;
+  if constexpr (persistent_block<TI, TJ, WMW, NS, OCC, MODE, LRS, LRDT, ODT, ACC>()) {
+    // one workgroup per CU; each XCD's share of workgroups claims that XCD's tiles (see the kernel)
+    const int wg = persistent_workgroups();
+    if (wg > 0 && grid.x > (unsigned)wg) {
+      grid.x = (unsigned)wg;
+      if (a.sched_alloc) a.sched = stream_sched(stream);
+    }
+  }
   hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, WMW, NS, OCC, PACKED, MODE, LRS, LRDT, ODT, ACC>), grid, dim3(128 * WMW), 0,
                      stream, a);
   return check_launch("int8_gemm");
@@ -924,6 +1070,7 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
   args.c = c; args.out_row_idx = out_row_idx; args.c_rows = c_rows;
   args.lda = lda; args.ldw = ldw; args.ldt = ldt; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K; args.R = (int)R;
+  args.sched_alloc = true;
   if (group == 32) return dispatch_dtypes<false, kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
   return dispatch_dtypes<false, kModeChannel>(args, has_lr, lr_dtype, out_dtype, stream);
 }
@@ -945,11 +1092,10 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
   return launch_dma<2, 2, 2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
 }
 
-extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
-                                   int64_t group, const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R,
-                                   int32_t lr_dtype, void* c, int64_t ldc, int32_t out_dtype,
-                                   const int32_t* out_row_idx, int64_t c_rows, int64_t M, int64_t N, int64_t K,
-                                   hipStream_t stream) {
+int pq::int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w, int64_t group,
+                         const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
+                         void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows,
+                         int64_t M, int64_t N, int64_t K, hipStream_t stream, bool sched_alloc) {
   const bool accumulate = (out_dtype & PQ_ACCUMULATE) != 0;
   out_dtype &= ~PQ_ACCUMULATE;
   if (M < 0 || N < 1 || K < 1) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: bad shape");
@@ -965,6 +1111,7 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
   GemmArgs args{};
   args.a = ap; args.w = wp; args.c = c;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
+  args.sched_alloc = sched_alloc;
   if (accumulate && (out_dtype == PQ_I32 || group != 0))
     return set_error(PQ_EINVAL, "pq_int8_gemm_packed: PQ_ACCUMULATE takes a 16-bit output and per-channel weights");
   if (out_dtype == PQ_I32) {
@@ -1004,4 +1151,13 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
   if (group == 32) return dispatch_dtypes<true, kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
   if (accumulate) return dispatch_dtypes<true, kModeChannel, true>(args, has_lr, lr_dtype, out_dtype, stream);
   return dispatch_dtypes<true, kModeChannel>(args, has_lr, lr_dtype, out_dtype, stream);
+}
+
+extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w,
+                                   int64_t group, const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R,
+                                   int32_t lr_dtype, void* c, int64_t ldc, int32_t out_dtype,
+                                   const int32_t* out_row_idx, int64_t c_rows, int64_t M, int64_t N, int64_t K,
+                                   hipStream_t stream) {
+  return pq::int8_gemm_packed(ap, wp, s_row, s_w, group, bias, t, ldt, l2t, R, lr_dtype, c, ldc, out_dtype, out_row_idx,
+                              c_rows, M, N, K, stream, true);
 }

@@ -34,7 +34,8 @@ LayerSlices layer_slices(int64_t M, int64_t K, int64_t R) {
 // The layer over a workspace the caller provides (shared by pq_int8_linear and its allocation-free variant).
 static int run_layer(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
                      const float* s_w, int64_t group, const float* bias, const void* l1t, const void* l1f, int64_t R,
-                     const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N, uint8_t* ws, hipStream_t stream) {
+                     const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N, uint8_t* ws, hipStream_t stream,
+                     bool sched_alloc) {
   const LayerSlices sl = layer_slices(M, K, R);
   int8_t* const q = reinterpret_cast<int8_t*>(ws);
   float* const s = reinterpret_cast<float*>(ws + sl.scales);
@@ -42,8 +43,8 @@ static int run_layer(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64
   int st = R ? pq_quant_rows_lowrank(x, x_dtype, M, K, ldx, M, nullptr, l1t, l1f, R, q, s, t, R, stream)
              : pq_quant_rows_packed(x, x_dtype, M, K, ldx, M, nullptr, q, s, stream);
   if (st != PQ_OK) return st;
-  return pq_int8_gemm_packed(q, w_packed, s, s_w, group, bias, R ? t : nullptr, R, R ? l2t : nullptr, Re, x_dtype, y,
-                             ldy, x_dtype, nullptr, 0, M, N, K, stream);
+  return int8_gemm_packed(q, w_packed, s, s_w, group, bias, R ? t : nullptr, R, R ? l2t : nullptr, Re, x_dtype, y, ldy,
+                          x_dtype, nullptr, 0, M, N, K, stream, sched_alloc);
 }
 
 int check_layer(int64_t M, int64_t K, int64_t N, int64_t R, int64_t Re, const void* l1t, const void* l2t,
@@ -79,7 +80,7 @@ extern "C" int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t
                      (long long)need);
   if ((uintptr_t)workspace % 256) return set_error(PQ_EALIGN, "pq_int8_linear: the workspace must be 256-byte aligned");
   return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, l1f, R, l2t, Re, y, ldy, N,
-                   static_cast<uint8_t*>(workspace), stream);
+                   static_cast<uint8_t*>(workspace), stream, true);
 }
 
 // ---- allocation-free variant -------------------------------------------------------------------------------------
@@ -142,5 +143,7 @@ extern "C" int pq_int8_linear_noalloc(const void* x, int32_t x_dtype, int64_t M,
   uint8_t* ws = nullptr;
   st = device_scratch(stream, &ws);
   if (st != PQ_OK) return st;
-  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, l1f, R, l2t, Re, y, ldy, N, ws, stream);
+  // no scheduling buffer either: a large GEMM keeps the static schedule (nothing is allocated)
+  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, l1f, R, l2t, Re, y, ldy, N, ws, stream,
+                   false);
 }
