@@ -34,6 +34,7 @@
 // workgroup per CU, which claims its XCD's tiles (then the other XCDs') through a per-stream scheduling buffer.
 #include "pq_common.h"
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <type_traits>
@@ -874,20 +875,23 @@ constexpr int ring_stages() {
 // Compute units of the current device, rounded down to a multiple of the 8 XCDs (a persistent grid keeps workgroup
 // b on XCD b % 8); 0 if unknown.
 int persistent_workgroups() {
-  static int cached[64];
+  static std::atomic<int> cached[64];
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
     (void)hipGetLastError();
     return 0;
   }
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
     (void)hipGetLastError();
     return 0;
   }
   cus &= ~7;
-  if (dev < 64) cached[dev] = cus;
+  if (dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 
