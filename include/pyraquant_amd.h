@@ -130,8 +130,8 @@ int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t 
  * R in {16, 32, 64}; group 32 needs N * K < 2^33 (its scales are read at 32-bit buffer offsets);
  * lr_dtype and out_dtype are PQ_BF16 or PQ_F16; out_row_idx entries unique (two rows naming one row of c race).
  * Large products (rank 0-32, no accumulate, more 256 x 256 blocks than CUs) run one persistent workgroup per CU
- * that claims blocks from per-XCD counters in a 36-byte device buffer belonging to the calling thread's device and
- * the stream: the library allocates it on the first such launch on that stream (never while the stream is being
+ * that claims blocks from per-XCD counters in a 36-byte buffer on the stream's device, belonging to the stream:
+ * the library allocates it on the first such launch on that stream (never while the stream is being
  * captured, and in relaxed capture mode), and each launch leaves it zeroed for the next. Launches on different
  * streams never share one. A stream being captured gets a fixed share of blocks per workgroup instead, as does
  * pq_int8_linear_noalloc, so a graph replays without the buffer. The results do not depend on the schedule.

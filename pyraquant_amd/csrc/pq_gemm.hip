@@ -872,12 +872,12 @@ constexpr int ring_stages() {
   return ns < 8 ? ns : 8;
 }
 
-// Compute units of the current device, rounded down to a multiple of the 8 XCDs (a persistent grid keeps workgroup
+// Compute units of the stream's device, rounded down to a multiple of the 8 XCDs (a persistent grid keeps workgroup
 // b on XCD b % 8); 0 if unknown.
-int persistent_workgroups() {
+int persistent_workgroups(hipStream_t stream) {
   static std::atomic<int> cached[64];
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0) {
     (void)hipGetLastError();
     return 0;
   }
@@ -908,8 +908,9 @@ int* stream_sched(hipStream_t stream) {
     return nullptr;
   }
   if (cs != hipStreamCaptureStatusNone) return nullptr;
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess) {
+  // the stream's device holds the buffer (the kernel runs there, whichever device is current)
+  int dev = -1, cur = -1;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || hipGetDevice(&cur) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
@@ -926,12 +927,17 @@ int* stream_sched(hipStream_t stream) {
     return nullptr;
   }
   int* buf = nullptr;
-  hipError_t e = hipMalloc(reinterpret_cast<void**>(&buf), 9 * sizeof(int));
+  hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&buf), 9 * sizeof(int));
   if (e == hipSuccess) e = hipMemsetAsync(buf, 0, 9 * sizeof(int), stream);
+  if (e != hipSuccess && buf) {
+    (void)hipFree(buf);
+    buf = nullptr;
+  }
+  if (dev != cur) (void)hipSetDevice(cur);
   (void)hipThreadExchangeStreamCaptureMode(&mode);
   if (e != hipSuccess) {
     (void)hipGetLastError();
-    if (buf) (void)hipFree(buf);
     return nullptr;
   }
   bufs.emplace(key, buf);
@@ -947,7 +953,7 @@ int launch_dma(GemmArgs& a, hipStream_t stream) {
   a.sched = nullptr;
   if constexpr (persistent_block<TI, TJ, WMW, NS, OCC, MODE, LRS, LRDT, ODT, ACC>()) {
     // one workgroup per CU; each XCD's share of workgroups claims that XCD's tiles (see the kernel)
-    const int wg = persistent_workgroups();
+    const int wg = persistent_workgroups(stream);
     if (wg > 0 && grid.x > (unsigned)wg) {
       grid.x = (unsigned)wg;
       if (a.sched_alloc) a.sched = stream_sched(stream);
