@@ -18,9 +18,12 @@ pytestmark = pytest.mark.gpu
 
 # 256 x 256 blocks: 16 x 32 = 512 tiles, more than the 256 CUs (persistent); 128 x 256 blocks: 1024 (large tiles)
 M, N, K = 4096, 8192, 512
+# ragged: 17 x 31 = 527 tiles (527 % 8 = 7: the XCD lists differ in length by one), the last tile column 0.75 wide
+RAGGED = (4352, 7936, 384)
 
 
-def _problem(cuda, seed, lr):
+def _problem(cuda, seed, lr, shape=(M, N, K)):
+    M, N, K = shape
     from pyraquant_amd import int8_exec as E
 
     g = torch.Generator().manual_seed(seed)
@@ -33,12 +36,14 @@ def _problem(cuda, seed, lr):
     if lr:
         t = (torch.randn(M, lr, generator=g) * 0.5).to(torch.bfloat16).to(cuda)
         l2t = (torch.randn(N, lr, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
-    return dict(ap=E.pack_k64(a.to(cuda)), wp=E.pack_k64(w.to(cuda)), s_row=s_row, s_w=s_w, bias=bias, t=t, l2t=l2t)
+    return dict(ap=E.pack_k64(a.to(cuda)), wp=E.pack_k64(w.to(cuda)), s_row=s_row, s_w=s_w, bias=bias, t=t, l2t=l2t,
+                shape=(M, N, K))
 
 
 def _run(P, out):
     from pyraquant_amd import int8_exec as E
 
+    M, N, K = P["shape"]
     return E.int8_gemm_packed(P["ap"], P["s_row"], P["wp"], P["s_w"], P["bias"], M, N, K, torch.bfloat16,
                               t=P["t"], l2t=P["l2t"], out=out)
 
@@ -48,6 +53,7 @@ def _sliced(P):
     [r0 K, (r0 + 256) K), r0 a multiple of 16)."""
     from pyraquant_amd import int8_exec as E
 
+    M, N, K = P["shape"]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=P["ap"].device)
     for r0 in range(0, M, 256):
         t = None if P["t"] is None else P["t"][r0:r0 + 256]
@@ -56,16 +62,16 @@ def _sliced(P):
     return out
 
 
-@pytest.mark.parametrize("lr", [0, 32])
-def test_consecutive_launches_write_every_tile(cuda, lr):
-    P = _problem(cuda, 11 + lr, lr)
+@pytest.mark.parametrize("lr,shape", [(0, (M, N, K)), (32, (M, N, K)), (32, RAGGED)])
+def test_consecutive_launches_write_every_tile(cuda, lr, shape):
+    P = _problem(cuda, 11 + lr, lr, shape)
     ref = _sliced(P)
-    out = torch.empty((M, N), dtype=torch.bfloat16, device=cuda)
+    out = torch.empty(shape[:2], dtype=torch.bfloat16, device=cuda)
     for i in range(5):
         out.fill_(float("nan"))
         _run(P, out)
         torch.cuda.synchronize()
-        print(f"[persistent] lr={lr} launch {i}", flush=True)
+        print(f"[persistent] lr={lr} shape={shape} launch {i}", flush=True)
         assert not torch.isnan(out).any(), f"launch {i}: tiles left unwritten"
         assert torch.equal(out, ref), f"launch {i}"
 
