@@ -964,17 +964,28 @@ int launch_dma(GemmArgs& a, hipStream_t stream) {
   return check_launch("int8_gemm");
 }
 
-// Tile choice of the LDS-DMA kernel. Large problems (at least 1024 blocks of 256 x 128): 256 x 256 blocks of 8 waves
-// at one workgroup per CU, a third less LDS-DMA traffic per MFMA than two 256 x 128 workgroups of 4 waves (measured
-// in the layer's back-to-back step, interleaved on one box: 2 % faster at K = 3072, 6 % at K = 12288). Otherwise
-// 128 x 128 blocks at two per CU (17 % faster than one per CU at M = 4096, K = N = 3072), and 128 x 64 blocks when
-// even those are too few to fill the chip.
-inline bool big_tiles(const GemmArgs& a) {
-  const int64_t tiles = (int64_t)((a.M + 127) / 128) * ((a.N + 255) / 256);
-  return tiles >= 1024;
-}
 // 128 x 128 blocks of the problem (the small-problem tile).
 inline int64_t small_blocks(const GemmArgs& a) { return (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128); }
+
+// Tile choice of the LDS-DMA kernel: 256 x 256 blocks of 8 waves at one workgroup per CU, or 128 x 128 blocks of 4
+// waves at two per CU (or 128 x 64 when even those are too few to fill the chip).
+// * Large problems (at least 1024 blocks of 256 x 128) take 256 x 256 blocks: a third less LDS-DMA traffic per MFMA
+//   than two 256 x 128 workgroups of 4 waves (measured in the layer's back-to-back step, interleaved on one box: 2 %
+//   faster at K = 3072, 6 % at K = 12288).
+// * So do problems whose 256 x 256 blocks all fit in one round (at most one per CU) while their 128 x 128 blocks
+//   would need more than one round of two per CU. A 256 x 256 block takes about 3x the time of a 128 x 128 block for
+//   4x its work, so one round of them beats the extra round of small blocks. Measured at M = 4352 (FLUX's 1K token
+//   count), bit-identical outputs: 56.7 -> 45.2 us at K = N = 3072, 182 -> 150 us at K = 12288, N = 3072, 226 ->
+//   179 us at K = 15360; at M = 4096, K = N = 3072: 46.0 -> 44.4 us. Where the 128 x 128 blocks fit in one round
+//   (M = 2048) or the 256 x 256 ones need a second (M = 8192), 128 x 128 stays faster (27.7 against 35.9 us, 92
+//   against 94.6 us).
+inline bool big_tiles(const GemmArgs& a, hipStream_t stream) {
+  const int64_t tiles = (int64_t)((a.M + 127) / 128) * ((a.N + 255) / 256);
+  if (tiles >= 1024) return true;
+  const int64_t cus = persistent_workgroups(stream);
+  const int64_t big = (int64_t)((a.M + 255) / 256) * ((a.N + 255) / 256);
+  return cus > 0 && big <= cus && small_blocks(a) > 2 * cus;
+}
 
 template <bool PACKED, int MODE, int LRS, int LRDT, int ODT, bool ACC>
 int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
@@ -991,7 +1002,7 @@ int dispatch_tiles(GemmArgs& a, hipStream_t stream) {
       return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
     }
   } else {
-    if (big_tiles(a)) return launch_dma<4, 2, 4, 1, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
+    if (big_tiles(a, stream)) return launch_dma<4, 2, 4, 1, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
     // fewer 128 x 128 blocks than half the CUs: 128 x 64 blocks (measured 1.3x faster at 80 blocks, even at 160)
     if (small_blocks(a) < 128) return launch_dma<2, 1, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
     return launch_dma<2, 2, 2, 2, PACKED, MODE, LRS, LRDT, ODT, ACC>(a, stream);
@@ -1098,7 +1109,7 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
   args.a = a; args.w = w; args.c = c;
   args.lda = lda; args.ldw = ldw; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
-  if (big_tiles(args)) return launch_dma<4, 2, 4, 1, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+  if (big_tiles(args, stream)) return launch_dma<4, 2, 4, 1, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
   return launch_dma<2, 2, 2, 2, false, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
 }
 
@@ -1129,7 +1140,7 @@ int pq::int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row,
       return set_error(PQ_EALIGN, "pq_int8_gemm_packed: int32 c must be 16-byte aligned with ldc %% 4 == 0");
     if (ldc > 0x7fffffffLL) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: ldc %lld is 2^31 or more", (long long)ldc);
     args.ldc = ldc;
-    if (big_tiles(args)) return launch_dma<4, 2, 4, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
+    if (big_tiles(args, stream)) return launch_dma<4, 2, 4, 1, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
     return launch_dma<2, 2, 2, 2, true, kModeI32, 0, PQ_BF16, PQ_BF16>(args, stream);
   }
   if (!s_row || !s_w) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null s_row / s_w");

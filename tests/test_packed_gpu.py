@@ -236,6 +236,39 @@ def test_gemm_packed_group32_lowrank_scatter(oracle, cuda, lr):
     assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
 
 
+@pytest.mark.parametrize("M,N,K,lr", [(4352, 3072, 3072, 32), (4100, 3008, 1280, 0), (3000, 3072, 12288, 32)])
+def test_gemm_one_round_big_tiles(oracle, cuda, M, N, K, lr):
+    """Problems whose 256 x 256 blocks all fit in one round on the chip (at most one per CU) while their 128 x 128
+    blocks would need more than one round take the 256 x 256 block (M = 4352 is FLUX's 1K token count; the others
+    are ragged in M and N, and long in K). The int32 accumulators are exact against the oracle on sampled rows, the
+    last ragged ones included, row-major and packed. The fused output is bit-identical to the same product computed
+    in 256-row slices, whose few blocks run the 128 x 64 kernel with the same per-element epilogue arithmetic."""
+    from pyraquant_amd import int8_exec as E
+
+    a, w = _codes(M, N, K, M + N + lr, cuda)
+    ap, wp = E.pack_k64(a), E.pack_k64(w)
+    c = E.int8_gemm_i32(a, w)
+    assert torch.equal(c, E.int8_gemm_packed(ap, None, wp, None, None, M, N, K, torch.int32))
+    g = torch.Generator().manual_seed(lr + 5)
+    sample = torch.cat([torch.arange(M - 40, M), torch.randperm(M - 40, generator=g)[:24]]).sort().values.to(cuda)
+    assert np.array_equal(c[sample].cpu().numpy(), oracle.gemm_i32(a[sample].cpu().numpy(), w.cpu().numpy()))
+    s_row = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(cuda)
+    s_w = (torch.rand(N, generator=g) * 2e-4 + 1e-5).to(cuda)
+    bias = (torch.randn(N, generator=g) * 0.01).to(cuda)
+    t = l2t = None
+    if lr:
+        t = (torch.randn(M, lr, generator=g) * 0.5).to(torch.bfloat16).to(cuda)
+        l2t = (torch.randn(N, lr, generator=g) * 0.02).to(torch.bfloat16).to(cuda)
+    got = E.int8_gemm_packed(ap, s_row, wp, s_w, bias, M, N, K, torch.bfloat16, t=t, l2t=l2t)
+    ref = torch.empty_like(got)
+    for r0 in range(0, M, 256):     # rows r0 .. r0 + 255 of a packed operand are its bytes [r0 K, (r0 + 256) K)
+        r1 = min(r0 + 256, M)
+        E.int8_gemm_packed(ap[r0 * K:], s_row[r0:], wp, s_w, bias, r1 - r0, N, K, torch.bfloat16,
+                           t=None if t is None else t[r0:r1], l2t=l2t, out=ref[r0:r1])
+    assert torch.equal(got, ref)
+    assert torch.equal(E._gemm(a, s_row, w, s_w, 0, bias, t, l2t, torch.bfloat16), got)
+
+
 @pytest.mark.parametrize("M,N,K,lr", [(4352, 12288, 3072, 0), (4352, 12288, 3072, 32), (2100, 9216, 1280, 0)])
 def test_gemm_big_tile_rowmajor_equals_packed_repeated(cuda, M, N, K, lr):
     """256 x 256 blocks on row-major operands (the reference self-test's int8_gemm_fused shape) give the packed path's

@@ -177,14 +177,15 @@ def test_load_method_weights_package(cuda, tmp_path):
     assert rel < 2e-2, rel
 
 
-@pytest.mark.parametrize("M,lowrank", [(300, 0), (300, 32), (4352, 32), (65792, 32)])
+@pytest.mark.parametrize("M,lowrank", [(300, 0), (300, 32), (2100, 32), (4352, 32), (65792, 32)])
 def test_split_linear_accumulates_in_epilogue(oracle, cuda, M, lowrank):
     """The FLUX single-block proj_out split along its input (K = 3072 + 12288 -> N = 3072), both halves Int8Linear:
     the second half adds its result into the first half's output inside its GEMM epilogue (PQ_ACCUMULATE). That is
     bit-identical to torch's y0 + y1 of the two halves' outputs; without a low-rank branch it is bit-identical to the
     oracle's two layers summed with one 16-bit rounding (round(round(y0) + round(y1))), and with one it is within
-    the tolerance of the oracle's fp32 sum, on 104 sampled rows (the last 40 included) at every M: 300 and 4352 run
-    the 128-wide tiles, 65792 (FLUX 4K, 4096^2 image + 256 text tokens) the 256 x 256 tiles."""
+    the tolerance of the oracle's fp32 sum, on 104 sampled rows (the last 40 included) at every M: 300 runs 128 x 64
+    blocks, 2100 128 x 128 blocks, 4352 (FLUX 1K) one round of 256 x 256 blocks and 65792 (FLUX 4K, 4096^2 image +
+    256 text tokens) persistent 256 x 256 blocks."""
     from conftest import MAX_REL, MEAN_REL, bits, elem_violation, rel_errors
     from pyraquant_amd import int8_exec as E
     from pyraquant_amd import weights
