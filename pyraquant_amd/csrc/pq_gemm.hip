@@ -546,6 +546,11 @@ void gemm_dma_kernel(const GemmArgs p) {
   tile_coords<group_m<OCC>()>(vb, nbt, p.tiles_m, p.tiles_n, tm, tn);
   const int m0 = tm * BM;
   const int n0 = tn * BN;
+  // Persistent blocks: alternate rounds of an XCD's tiles (round = local index / workgroups per XCD) sweep K in
+  // opposite directions. The raster's consecutive rounds share their m-tiles' A rows, so a reversed round starts on
+  // the K range the previous round read last, which is still in the L2: 15 % fewer bytes fetched beyond the L2 at
+  // c1 (3.79 -> 3.23 GB), the same time. The int32 sums do not depend on the order.
+  const bool rev = PERSIST && (((vb >> 3) / max(1, (int)(gridDim.x >> 3))) & 1);
 
   // Buffer resources based at the block's first row. Rows past M / N, and the DMA of a stage past the end of K
   // (offset kOOB), lie outside num_records: those loads read no memory.
@@ -593,7 +598,7 @@ void gemm_dma_kernel(const GemmArgs p) {
 
   auto dma = [&](int buf, int kt) {
     uint8_t* sb = smem + buf * STAGE;
-    const int koff = kt < KT ? kt * kStageStep : kOOB;
+    const int koff = kt < KT ? (rev ? KT - 1 - kt : kt) * kStageStep : kOOB;
 #pragma unroll
     for (int i = 0; i < DW; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, (lds_void_t*)(sb + (wave * DW + i) * 1024), 16,
