@@ -66,13 +66,19 @@ __device__ __forceinline__ v2u quant_chunk(v4u v, float s, float rc) {
   return v2u{low_bytes4(m[0], m[1], m[2], m[3]), low_bytes4(m[4], m[5], m[6], m[7])};
 }
 
+// Maximum over the 64 lanes of a wave, for values below 2^31, in DPP row operations (no LDS round trip): quad_perm
+// [1,0,3,2] and [2,3,0,1] within groups of 4 lanes, the half-row and row mirrors within 8 and 16, then row_bcast:15
+// (lane 15 of rows 0 and 2 into rows 1 and 3) and row_bcast:31 (lane 31 into rows 2 and 3), after which lane 63
+// holds the maximum of all 64; readlane makes it wave-uniform.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t o = (uint32_t)__shfl_xor((int)v, off, 64);
-    v = v > o ? v : o;
-  }
-  return v;
+  int x = (int)v;
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0xb1, 0xf, 0xf, false));    // quad_perm [1,0,3,2]
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x4e, 0xf, 0xf, false));    // quad_perm [2,3,0,1]
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x141, 0xf, 0xf, false));   // row_half_mirror
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x140, 0xf, 0xf, false));   // row_mirror
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x142, 0xa, 0xf, false));   // row_bcast:15 -> rows 1, 3
+  x = max(x, __builtin_amdgcn_update_dpp(x, x, 0x143, 0xc, 0xf, false));   // row_bcast:31 -> rows 2, 3
+  return (uint32_t)__builtin_amdgcn_readlane(x, 63);
 }
 
 // Magnitude bits of a 16-bit float pair -> fp32 of the larger magnitude.
