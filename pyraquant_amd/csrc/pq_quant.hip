@@ -616,12 +616,15 @@ __global__ __launch_bounds__(256) void pack_lowrank_l1t_kernel(const v4u* __rest
   dst[p] = src[(row * K + col) / 8];
 }
 
-// ---- fused quantizer + low-rank down-projection for wide rows (K = 4096 .. 12288) ---------------------------------
+// ---- fused quantizer + low-rank down-projection for wide rows (K = 4096 .. 12288, and 15360) ----------------------
 // The same results as quant_lowrank_kernel (codes and scales of pq_quant_rows_packed, t = x @ L1 rounded to 16 bits)
 // for rows too wide for its LDS staging (c2a: K = 12288, a 16-row batch is 384 KB). x is read from HBM once: a
 // re-read of a batch runs at HBM speed even when the memory-side cache holds it, so reading twice costs twice.
-// One workgroup of 8 waves per CU, persistent over batches of 16 rows; wave w holds rows 2 w and 2 w + 1 of the batch
-// whole in registers (NCH 16-byte chunks per lane per row, the row-per-wave load pattern of quant_rows_vec_kernel).
+// One workgroup of 8 waves per CU, persistent over batches of 8 RPW rows; wave w holds rows RPW w .. RPW w + RPW - 1
+// of the batch whole in registers (NCH 16-byte chunks per lane per row, the row-per-wave load pattern of
+// quant_rows_vec_kernel). RPW = 2 up to K = 12288 (192 registers of row data per lane); RPW = 1 for K = 15360 (FLUX's
+// single-block proj_out, 3072 + 12288: two rows would need 240), whose 8-row batches fill half of the MFMA's 16
+// columns (the other half, zeros, is computed and discarded) and half of a 16-row packed block each.
 // Per batch: the absmax and scale of each row from the registers (a wave reduction; the IEEE steps of
 // quant_rows_vec_kernel); then for each 512-wide K slab e:
 //   a. the wave writes its two rows' chunk e into the x slab buffer (16 rows, double buffered);
@@ -635,20 +638,23 @@ __global__ __launch_bounds__(256) void pack_lowrank_l1t_kernel(const v4u* __rest
 // loads chunk e of its next batch into the same registers, so the next rows stream in under this batch's work.
 // Ordering: the L1^T DMA of slab e + 1 is issued after barrier e, when every wave has read that buffer's previous slab
 // (e - 1); it must land before barrier e + 1, and the only vector-memory instructions issued after it are slab e + 1's
-// two code stores and two next-batch loads, hence vmcnt(4) there (vector-memory instructions retire in issue order).
+// RPW code stores and RPW next-batch loads, hence vmcnt(2 RPW) there (vector-memory instructions retire in issue
+// order).
 // Past the last batch the next-batch loads read this batch's rows again (discarded), which keeps that count exact.
 constexpr int kWideWaves = 8;                 // waves per workgroup, two rows each: batches of 16 rows
 constexpr int kWideSlab = 512;                // K elements per slab
 constexpr int kWidePitch = 2 * kWideSlab + 16;   // LDS row pitch: consecutive rows 16 bytes apart in the bank window
 constexpr int kWideRedPitch = 36;             // floats per row of the partial-sum buffer
 
-template <int DT, int NCH>   // NCH = K / 512: 16-byte chunks per lane per row, and slabs
+template <int DT, int NCH, int RPW>   // NCH = K / 512: 16-byte chunks per lane per row, and slabs; RPW rows per wave
 __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int64_t M, const int32_t* __restrict__ row_idx,
     const uint16_t* __restrict__ l1t, int8_t* __restrict__ qp, float* __restrict__ s, uint16_t* __restrict__ t,
     int64_t ldt, int nbatch) {
   constexpr int K = 512 * NCH;
   constexpr int KW = kWideSlab / kWideWaves;   // 64: each wave's share of a slab, two MFMA K steps
+  constexpr int BR = kWideWaves * RPW;         // rows per batch (16 or 8)
+  static_assert(RPW == 1 || RPW == 2, "rows per wave");
   // double buffers as separate arrays, so that the compiler can tell an LDS read of one buffer from a pending
   // LDS-DMA into the other (it waits for every DMA that may alias a read)
   __shared__ __attribute__((aligned(1024))) uint8_t lbuf0[32 * kWidePitch], lbuf1[32 * kWidePitch];   // L1^T slabs
@@ -658,6 +664,13 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // MFMA 16x16x32 operands: lane l feeds A row (L1^T row) and B column (batch row) l % 16, K group l / 16
   const int nr = lane & 15, kg = lane >> 4;
+  if constexpr (BR < 16) {
+    // x slab rows BR .. 15 feed MFMA columns whose results are discarded: zeros, never written again
+    for (int i = tid; i < (16 - BR) * kWidePitch / 16; i += 64 * kWideWaves) {
+      reinterpret_cast<v4u*>(xbuf0 + BR * kWidePitch)[i] = v4u{0u, 0u, 0u, 0u};
+      reinterpret_cast<v4u*>(xbuf1 + BR * kWidePitch)[i] = v4u{0u, 0u, 0u, 0u};
+    }
+  }
   const __amdgpu_buffer_rsrc_t rs_l =
       __builtin_amdgcn_make_buffer_rsrc((void*)l1t, (short)0, 32 * K * 2, kBufferWord3);
   // L1^T slab e -> lbuf[e & 1]: wave w copies rows 4 w .. 4 w + 3, one 1 KB LDS-DMA each; the slab's offset rides
@@ -674,7 +687,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
   // [0, x_rows) (both read as zeros: row 0 is loaded, harmlessly, and the data cleared before use). Wave-uniform:
   // the row bases stay in scalar registers and each lane adds its own 16-byte offset.
   auto src_of = [&](int bb, int rho) -> int64_t {
-    const int64_t m = (int64_t)bb * 16 + 2 * wave + rho;
+    const int64_t m = (int64_t)bb * BR + RPW * wave + rho;
     const int64_t src = m >= M ? -1 : (row_idx ? (int64_t)row_idx[m] : m);
     return src >= 0 && src < x_rows ? src : -1;
   };
@@ -682,18 +695,19 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
     const int64_t src = src_of(bb, rho);
     return reinterpret_cast<const v4u*>(x + (src < 0 ? 0 : src) * ldx);
   };
-  // this lane's byte offset inside a row's packed K64 codes, for the rows 2 w (rho = 0) and 2 w + 1 of a batch
-  int qlane[2];
-#pragma unroll
-  for (int rho = 0; rho < 2; ++rho)
-    qlane[rho] = (lane >> 3) * 1024 + ((((lane >> 1) & 3) ^ k64_swz(2 * wave + rho)) << 4) + (lane & 1) * 8;
-  v4u v[2][NCH];
+  // this lane's byte offset inside a row's packed K64 codes, for row r' (0 .. 15) of its 16-row block
+  auto qlane_of = [&](int rb) {
+    return (lane >> 3) * 1024 + ((((lane >> 1) & 3) ^ k64_swz(rb)) << 4) + (lane & 1) * 8;
+  };
+  v4u v[RPW][NCH];
   // live[rho]: row rho of the batch in hand has a source row (decided when its loads were issued, one batch ahead:
   // recomputing it per batch cost the K = 12288 kernel a spilled register)
-  bool live[2] = {false, false};
+  bool live[RPW];
+#pragma unroll
+  for (int rho = 0; rho < RPW; ++rho) live[rho] = false;
   if (blockIdx.x < nbatch) {
 #pragma unroll
-    for (int rho = 0; rho < 2; ++rho) {
+    for (int rho = 0; rho < RPW; ++rho) {
       live[rho] = src_of(blockIdx.x, rho) >= 0;
       const v4u* xr = src_row(blockIdx.x, rho);
 #pragma unroll
@@ -702,11 +716,11 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
   }
   for (int b = blockIdx.x; b < nbatch; b += gridDim.x) {
     const int bn = b + gridDim.x;   // the next batch (past the end: this batch's rows again, loaded and discarded)
-    int64_t mrow[2];
-    const v4u* xn[2];
+    int64_t mrow[RPW];
+    const v4u* xn[RPW];
 #pragma unroll
-    for (int rho = 0; rho < 2; ++rho) {
-      mrow[rho] = (int64_t)b * 16 + 2 * wave + rho;
+    for (int rho = 0; rho < RPW; ++rho) {
+      mrow[rho] = (int64_t)b * BR + RPW * wave + rho;
       xn[rho] = src_row(bn < nbatch ? bn : b, rho);
       if (!live[rho]) {   // a padding row or a gathered row outside x: it quantizes as zeros
 #pragma unroll
@@ -715,9 +729,9 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
       live[rho] = src_of(bn < nbatch ? bn : b, rho) >= 0;   // the batch whose loads xn starts
     }
     dma_l(0);   // lands before slab 0's barrier: only that slab's code stores and next-batch loads come after it
-    float sc[2], rc[2];
+    float sc[RPW], rc[RPW];
 #pragma unroll
-    for (int rho = 0; rho < 2; ++rho) {
+    for (int rho = 0; rho < RPW; ++rho) {
       us2 mx2 = {0, 0};
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
@@ -731,26 +745,31 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
       sc[rho] = __fdiv_rn(a, 127.0f);
       rc[rho] = __fdiv_rn(1.0f, sc[rho]);
     }
-    // packed K64 rows of the batch: block row b, row 2 w + rho inside it (k64_offset, split into the wave-uniform
-    // part and qlane)
-    int8_t* const qbatch = qp + (int64_t)b * (K / 64) * 1024 + 2 * wave * 64;
+    // packed K64 rows of the batch: rows b BR .. b BR + BR - 1 are rows (b BR) % 16 .. of block row b BR / 16, this
+    // wave's first row is row rb0 = (b BR) % 16 + RPW w of its block (k64_offset, split into the wave-uniform part
+    // and qlane)
+    const int rb0 = (b * BR) % 16 + RPW * wave;
+    int8_t* const qbatch = qp + (int64_t)b * BR / 16 * (K / 64) * 1024 + rb0 * 64;
+    int qlane[RPW];
+#pragma unroll
+    for (int rho = 0; rho < RPW; ++rho) qlane[rho] = qlane_of(rb0 + rho);
     v4f acc[2] = {v4f{}, v4f{}};   // t partial of this wave's K shares: D[r = 16 h + 4 kg + i][batch row nr]
 #pragma unroll
     for (int e = 0; e < NCH; ++e) {
       uint8_t* const xs = e & 1 ? xbuf1 : xbuf0;
       const uint8_t* const ls = e & 1 ? lbuf1 : lbuf0;
 #pragma unroll
-      for (int rho = 0; rho < 2; ++rho)
-        *reinterpret_cast<v4u*>(xs + (2 * wave + rho) * kWidePitch + lane * 16) = v[rho][e];
+      for (int rho = 0; rho < RPW; ++rho)
+        *reinterpret_cast<v4u*>(xs + (RPW * wave + rho) * kWidePitch + lane * 16) = v[rho][e];
       // codes of chunk e (padding rows past M hold zeros and quantize to zero codes): K elements 512 e + 8 lane ..
       // sit 8 packed blocks (8 KB) after those of chunk e - 1
 #pragma unroll
-      for (int rho = 0; rho < 2; ++rho)
+      for (int rho = 0; rho < RPW; ++rho)
         *reinterpret_cast<v2u*>(qbatch + rho * 64 + e * 8192 + qlane[rho]) = quant_chunk<DT>(v[rho][e], sc[rho], rc[rho]);
       // chunk e of the next batch into the registers just freed
 #pragma unroll
-      for (int rho = 0; rho < 2; ++rho) v[rho][e] = __builtin_nontemporal_load(xn[rho] + e * 64 + lane);
-      wait_vmcnt<4>();                      // this wave's DMA of L1^T slab e has landed (2 stores, 2 loads after it)
+      for (int rho = 0; rho < RPW; ++rho) v[rho][e] = __builtin_nontemporal_load(xn[rho] + e * 64 + lane);
+      wait_vmcnt<2 * RPW>();   // this wave's DMA of L1^T slab e has landed (RPW stores, RPW loads after it)
       __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's x slab writes are done
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_barrier();         // both slabs complete; every wave is done with slab e - 1
@@ -776,16 +795,16 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
     for (int h = 0; h < 2; ++h) *reinterpret_cast<v4f*>(&red[wave][nr][16 * h + 4 * kg]) = acc[h];
     if (lane == 0) {
 #pragma unroll
-      for (int rho = 0; rho < 2; ++rho)
+      for (int rho = 0; rho < RPW; ++rho)
         if (mrow[rho] < M) s[mrow[rho]] = sc[rho];
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();   // every wave's partials are in red (and every wave is done with the last slabs)
     __builtin_amdgcn_sched_barrier(0);
-    if (tid < 256) {
+    if (tid < 16 * BR) {
       const int n = tid >> 4, rr = (tid & 15) * 2;
-      const int64_t mo = (int64_t)b * 16 + n;
+      const int64_t mo = (int64_t)b * BR + n;
       float v0 = red[0][n][rr], v1 = red[0][n][rr + 1];
 #pragma unroll
       for (int w = 1; w < kWideWaves; ++w) {
@@ -929,8 +948,9 @@ extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t 
 }
 
 // Fused per-token quantizer (packed K64 codes) + rank-32 low-rank down-projection: the results of
-// pq_quant_rows_packed and pq_lowrank_down on the same x, with x read once where the fused kernel applies
-// (R == 32, K in {1024, 1280, 2048, 2560, 3072}, 16-byte aligned rows, 32-bit x offsets); otherwise the two.
+// pq_quant_rows_packed and pq_lowrank_down on the same x, with x read once where a fused kernel applies (R == 32,
+// 16-byte aligned rows, and K in {1024, 1280, 2048, 2560, 3072} with 32-bit x offsets, or K in {4096, 6144, 8192,
+// 10240, 12288, 15360}); otherwise the two.
 extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
                                      int64_t x_rows, const int32_t* row_idx, const void* l1t, const void* l1f,
                                      int64_t R, int8_t* qp, float* s, void* t, int64_t ldt, hipStream_t stream) {
@@ -943,25 +963,30 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
                      (row_idx || x_rows >= M) && x_rows * ldx * 2 + 2 * K <= 0x3fffffffLL &&
                      (uintptr_t)x % 16 == 0 && (uintptr_t)l1t % 16 == 0 && (uintptr_t)t % 4 == 0 &&
                      (uintptr_t)qp % 16 == 0 && (x_dtype == PQ_BF16 || x_dtype == PQ_F16);
-  // wide rows: one read of x through registers (quant_lowrank_wide_kernel)
-  const bool wide = !fused && R == 32 && K % 2048 == 0 && K >= 4096 && K <= 12288 && ldx >= K && ldx % 8 == 0 &&
+  // wide rows: one read of x through registers (quant_lowrank_wide_kernel), two rows per wave up to K = 12288, one at
+  // K = 15360
+  const bool wide = !fused && R == 32 && ((K % 2048 == 0 && K >= 4096 && K <= 12288) || K == 15360) && ldx >= K && ldx % 8 == 0 &&
                     ldt >= R && ldt % 2 == 0 && x_rows >= 1 && (row_idx || x_rows >= M) && (uintptr_t)x % 16 == 0 &&
                     (uintptr_t)l1t % 16 == 0 && (uintptr_t)t % 4 == 0 && (uintptr_t)qp % 16 == 0 &&
                     (x_dtype == PQ_BF16 || x_dtype == PQ_F16);
   if (wide) {
-    const int nbatch = (int)((M + 15) / 16);
+    // batches of 16 rows (two per wave) or 8 (one per wave), covering the packed padding rows up to a multiple of 16
+    const int rpw = K <= 12288 ? 2 : 1;
+    const int nbatch = (int)((M + 15) / 16) * (2 / rpw);
     const dim3 grid((unsigned)std::min(nbatch, 256));
     const uint16_t* xp = static_cast<const uint16_t*>(x);
     const uint16_t* lp = static_cast<const uint16_t*>(l1t);
     uint16_t* tp = static_cast<uint16_t*>(t);
-#define PQ_QWCASE(D, NCH)                                                                                      \
+#define PQ_QWCASE(D, NCH, RPW)                                                                                 \
     if (x_dtype == D && K == 512 * NCH) {                                                                      \
-      hipLaunchKernelGGL((quant_lowrank_wide_kernel<D, NCH>), grid, dim3(64 * kWideWaves), 0, stream, xp, ldx,    \
-                         x_rows, M, row_idx, lp, qp, s, tp, ldt, nbatch);                                      \
+      hipLaunchKernelGGL((quant_lowrank_wide_kernel<D, NCH, RPW>), grid, dim3(64 * kWideWaves), 0, stream, xp,    \
+                         ldx, x_rows, M, row_idx, lp, qp, s, tp, ldt, nbatch);                                 \
       return check_launch("quant_rows_lowrank");                                                               \
     }
-    PQ_QWCASE(PQ_BF16, 8) PQ_QWCASE(PQ_BF16, 12) PQ_QWCASE(PQ_BF16, 16) PQ_QWCASE(PQ_BF16, 20) PQ_QWCASE(PQ_BF16, 24)
-    PQ_QWCASE(PQ_F16, 8) PQ_QWCASE(PQ_F16, 12) PQ_QWCASE(PQ_F16, 16) PQ_QWCASE(PQ_F16, 20) PQ_QWCASE(PQ_F16, 24)
+    PQ_QWCASE(PQ_BF16, 8, 2) PQ_QWCASE(PQ_BF16, 12, 2) PQ_QWCASE(PQ_BF16, 16, 2) PQ_QWCASE(PQ_BF16, 20, 2)
+    PQ_QWCASE(PQ_BF16, 24, 2) PQ_QWCASE(PQ_BF16, 30, 1)
+    PQ_QWCASE(PQ_F16, 8, 2) PQ_QWCASE(PQ_F16, 12, 2) PQ_QWCASE(PQ_F16, 16, 2) PQ_QWCASE(PQ_F16, 20, 2)
+    PQ_QWCASE(PQ_F16, 24, 2) PQ_QWCASE(PQ_F16, 30, 1)
 #undef PQ_QWCASE
   }
   if (!fused) {

@@ -3,7 +3,8 @@
 * packed codes and scales bit-identical to pq_quant_rows_packed on the same rows (which the quantizer tests pin
   against the oracle);
 * t within bf16 rounding of the float64 product and within the build's tolerance of the oracle's fp32 result;
-* K = 4096 .. 12288 in steps of 2048 (c2a's 12288) run the wide kernel, which holds rows in registers: the same bar;
+* K = 4096 .. 12288 in steps of 2048 (c2a's 12288) and 15360 (FLUX's single-block proj_out) run the wide kernel,
+  which holds rows in registers (two per wave, one at 15360, in batches of 16 or 8 rows): the same bar;
 * other shapes (K outside both lists, R != 32) run the two kernels: the same bar, and exactly what the two separate
   entry points give;
 * the fragment-order copy of l1t (pq_pack_lowrank_l1t) matches its documented index formula, and the one-pass kernel
@@ -37,7 +38,8 @@ def _check_t(oracle, t, x_rows, l1, dtype):
 @pytest.mark.parametrize("M,K", [(1, 3072), (16, 3072), (17, 3072), (1000, 1280), (4099, 3072), (300, 2048),
                                  (65, 2560), (33, 1024), (20000, 3072),
                                  (1, 12288), (7, 12288), (1001, 12288), (37, 4096), (100, 5120), (50, 6144),
-                                 (23, 15360), (9000, 12288), (4111, 8192), (17, 10240)])
+                                 (23, 15360), (9000, 12288), (4111, 8192), (17, 10240),
+                                 (1, 15360), (8, 15360), (9, 15360), (16, 15360), (4352, 15360), (5003, 15360)])
 def test_quant_rows_lowrank_fused(oracle, cuda, dtype, M, K):
     from pyraquant_amd import int8_exec as E
     from pyraquant_amd.workloads import make_x
@@ -76,7 +78,7 @@ def test_quant_rows_lowrank_gather_view(oracle, cuda):
 
 
 @pytest.mark.parametrize("M,K,R", [(100, 5120, 32), (70, 640, 32), (300, 3072, 64), (40, 12288, 64),
-                                   (50, 15360, 32)])
+                                   (50, 14336, 32)])
 def test_quant_rows_lowrank_fallback(cuda, M, K, R):
     """Shapes outside the fused kernels' sets run the two kernels: identical to calling them one after the other."""
     from pyraquant_amd import int8_exec as E
@@ -90,13 +92,15 @@ def test_quant_rows_lowrank_fallback(cuda, M, K, R):
     assert torch.equal(t, E.lowrank_down(x, l1t))
 
 
-def test_quant_rows_lowrank_wide_gather_view(oracle, cuda):
-    """K = 12288 (the wide kernel) through a gather with duplicates and a row-slice view (ldx = K + 512): codes
-    and scales bit-identical to the packed quantizer's, t within bf16 rounding of the float64 product."""
+@pytest.mark.parametrize("K", [12288, 15360])
+def test_quant_rows_lowrank_wide_gather_view(oracle, cuda, K):
+    """K = 12288 and 15360 (the wide kernel, two and one rows per wave) through a gather with duplicates and a
+    row-slice view (ldx = K + 512): codes and scales bit-identical to the packed quantizer's, t within bf16 rounding
+    of the float64 product."""
     from pyraquant_amd import int8_exec as E
     from pyraquant_amd.workloads import make_x
 
-    rows, K, M = 600, 12288, 333
+    rows, M = 600, 333
     base = make_x(rows, K + 512, seed=9).to(cuda)
     x = base[:, 512:]
     g = torch.Generator().manual_seed(4)
@@ -110,18 +114,19 @@ def test_quant_rows_lowrank_wide_gather_view(oracle, cuda):
     _check_t(oracle, t, x.cpu()[idx.long()], l1, torch.bfloat16)
 
 
-def test_int8linear_uses_fused_pass(oracle, cuda):
-    """Int8Linear.forward at the c1 shape (reduced M) takes the fused pass: output within the tolerance of the
-    oracle from the same codes, and equal to the GEMM fed with the fused t."""
+@pytest.mark.parametrize("K,N,M", [(3072, 12288, 2000), (15360, 3072, 333)])
+def test_int8linear_uses_fused_pass(oracle, cuda, K, N, M):
+    """Int8Linear.forward takes the fused pass, at the c1 shape (reduced M) and at FLUX's unsplit single-block
+    proj_out (K = 15360, the wide kernel at one row per wave): output within the tolerance of the oracle from the same
+    codes, and equal to the GEMM fed with the fused t."""
     from pyraquant_amd import int8_exec as E
-    from pyraquant_amd.workloads import CONFIGS, make_linear, make_x
+    from pyraquant_amd.workloads import make_linear, make_x
 
-    c = CONFIGS["c1"]
-    q = E.Int8Linear(make_linear(c.K, c.N, c.lowrank, c.bias), device=cuda)
-    x = make_x(2000, c.K).to(cuda)
+    q = E.Int8Linear(make_linear(K, N, 32, True), device=cuda)
+    x = make_x(M, K).to(cuda)
     y = q(x)
     qp, sx, t = E.quant_rows_lowrank(x, q.lr_At)
-    ref = E.int8_gemm_packed(qp, sx, q.weight_packed, q.w_scale, q.bias, 2000, c.N, c.K, torch.bfloat16, t=t,
+    ref = E.int8_gemm_packed(qp, sx, q.weight_packed, q.w_scale, q.bias, M, N, K, torch.bfloat16, t=t,
                              l2t=q.lr_Bt)
     assert torch.equal(y, ref)
     o = oracle.linear(bits(x), 0, q.weight_int8.cpu().numpy(), q.w_scale.cpu().numpy(), q.bias.cpu().numpy(), 0,
