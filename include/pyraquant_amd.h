@@ -155,9 +155,10 @@ int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
  * t = x[rows] @ L1 (as pq_lowrank_down) from one pass over x: the two steps of Int8Linear.forward that read x,
  * `t = x2.to(lr_A.dtype) @ lr_A` and `quant_rows(x2)` (deploy/int8_exec.py:390-391). qp / s are bit-identical to
  * pq_quant_rows_packed; t is the fp32-accumulated product rounded to the 16-bit type, as pq_lowrank_down (the
- * accumulation order differs, so the last bit of t may differ from it). x is read from HBM once when R == 32,
- * K is one of 1024, 1280, 2048, 2560, 3072, rows are 16-byte aligned (ldx % 8 == 0) and every x byte offset fits
- * 30 bits; other shapes run the two kernels. l1t [R, K] contiguous, same dtype as x; t [M, R] with row stride ldt.
+ * accumulation order differs, so the last bit of t may differ from it). x is read from HBM once when R == 32, rows
+ * are 16-byte aligned (ldx % 8 == 0) and K is one of 1024, 1280, 2048, 2560, 3072 (rows staged through LDS; every x
+ * byte offset must fit 30 bits) or 4096, 6144, 8192, 10240, 12288, 15360 (rows held in registers); other shapes run
+ * the two kernels. l1t [R, K] contiguous, same dtype as x; t [M, R] with row stride ldt.
  * l1f: NULL, or the same matrix in the one-pass kernel's fragment order (pq_pack_lowrank_l1t, 16-byte aligned),
  * which that kernel then reads instead of l1t (contiguous 1 KB register loads: 15.8 -> 12.8 us at M = 4096,
  * K = 3072); results are identical either way, and l1t is still required (the other paths read it).
