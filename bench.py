@@ -608,7 +608,7 @@ def cpu_baseline(cfg, lin, rows: int, iters: int):
 def flux_linear_mix(dev):
     """The reference's own per-image micro-benchmark (deploy/int8_exec.py:539-571, run here by
     int8_exec.selftest_and_bench): for each token count M the four FLUX token-level Linear shapes, bf16 F.linear
-    against Int8Linear, summed with the per-image layer counts of FLUX_TOKEN_SHAPES (342 layers)."""
+    against Int8Linear, summed with the per-image layer counts of FLUX_TOKEN_SHAPES (418 layers)."""
     import contextlib
 
     from pyraquant_amd import int8_exec as E
@@ -620,7 +620,7 @@ def flux_linear_mix(dev):
         out[M] = {k: r[k] for k in ("bf16_ms", "int8_fused_ms", "quant_ms", "gemm_fused_ms", "speedup_fused_vs_bf16")}
         out[M]["per_shape_int8_ms"] = {k: v["int8_fused_ms"] for k, v in r["per_shape"].items()}
     return {"per_M": out, "selftest": res["selftest"],
-            "note": "ms per image for the 342 token-level Linears (per-shape mean x layer count); bf16 = torch F.linear "
+            "note": "ms per image for the 418 token-level Linears (per-shape mean x layer count); bf16 = torch F.linear "
                     "(hipBLASLt), int8 = Int8Linear.forward without low rank, as the reference's benchmark"}
 
 
