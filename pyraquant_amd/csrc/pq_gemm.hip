@@ -12,9 +12,10 @@
 // The kernel (gemm_dma_kernel). 2 x WMW wavefronts (WMW = 2 or 4 along m). A workgroup owns a BN x BM (n x m)
 // block, each wave a (BN/2) x (BM/WMW) part held as TI x TJ v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in
 // VGPRs: the kernels name no AGPR, so the compiler selects the MFMA form whose C / D operands are VGPRs, and the
-// epilogue reads the accumulators in place, with no v_accvgpr_read copies). Large problems run 256 x 256 blocks of
-// 8 waves at one workgroup per CU (128 accumulators per wave, two waves per SIMD); small ones 128 x 128 blocks of 4
-// waves at two workgroups per CU, or 128 x 64 when the 128 x 128 blocks are too few to fill the chip.
+// epilogue reads the accumulators in place, with no v_accvgpr_read copies). Large problems, and those whose 256 x 256
+// blocks all fit on the CUs at once while their 128 x 128 blocks would not, run 256 x 256 blocks of 8 waves at one
+// workgroup per CU (128 accumulators per wave, two waves per SIMD); smaller ones 128 x 128 blocks of 4 waves at two
+// workgroups per CU, or 128 x 64 when the 128 x 128 blocks are too few to fill the chip.
 // K advances in stages of 64 bytes through a ring of NS LDS stages (5 x 32 KB for the 256 x 256 block) filled by
 // LDS-DMA buffer loads (buffer_load_dwordx4 ... lds): no VGPR staging, no ds_write, and NS - 1 stages of
 // prefetch in flight to cover L2 / MALL latency. One DMA instruction fills 1 KB = 16 LDS rows of 64 bytes;
