@@ -110,3 +110,100 @@ def test_int8linear_random_sweep(oracle, cuda, i):
         finally:
             E.DIRECT_CALLS = True
         assert torch.equal(y, y2)
+
+
+# Large shapes: the 128 x 128 sweep above never reaches the 256 x 256 blocks (one round, or persistent over several),
+# so a second seeded family draws M and N large enough for them, with the same options, and checks sampled rows (the
+# last 40 included: the ragged tiles) against the oracle.
+N_BIG = 16
+
+
+def _big_case(i):
+    rng = np.random.default_rng(9000 + i)
+    lo = i % 2 == 0   # even cases about one round of 256 x 256 blocks, odd ones several
+    return dict(dtype=(torch.bfloat16, torch.float16)[int(rng.integers(2))],
+                K=int(rng.choice((256, 512, 1024, 1280, 3072))),
+                N=64 * int(rng.integers(24, 65) if lo else rng.integers(48, 129)),
+                M=int(rng.integers(2048, 5001) if lo else rng.integers(6000, 16385)),
+                group=32 if rng.random() < 0.25 else 0,
+                R=int(rng.choice((0, 16, 32, 32, 64))), bias=bool(rng.random() < 0.7), pad=int(rng.choice((0, 8))),
+                routed=bool(rng.random() < 0.35))
+
+
+def test_big_sweep_reaches_the_large_tiles():
+    """The large cases take each of the GEMM's block choices on a 256-CU part (the library's rule): persistent
+    256 x 256 blocks (at least 1024 blocks of 256 x 128, more 256 x 256 blocks than CUs), one round of 256 x 256
+    blocks (at most one per CU, where 128 x 128 blocks would exceed two per CU), 128 x 128 blocks, and group-32."""
+    kinds = []
+    for i in range(N_BIG):
+        c = _big_case(i)
+        M, N = c["M"], c["N"]
+        b128, b256, b256x128 = -(-M // 128) * -(-N // 128), -(-M // 256) * -(-N // 256), -(-M // 128) * -(-N // 256)
+        if c["group"]:
+            kinds.append("group-32")
+        elif b256x128 >= 1024:
+            kinds.append("persistent" if b256 > 256 else "256")
+        elif b256 <= 256 and b128 > 512:
+            kinds.append("one round")
+        else:
+            kinds.append("128")
+    for k in ("persistent", "one round", "128", "group-32"):
+        assert kinds.count(k) >= (3 if k in ("persistent", "one round") else 1), kinds
+
+
+@pytest.mark.parametrize("i", range(N_BIG))
+def test_int8linear_random_sweep_large(oracle, cuda, i):
+    from conftest import elem_violation
+    from pyraquant_amd import int8_exec as E
+
+    c = _big_case(i)
+    K, N, M, dt, R = c["K"], c["N"], c["M"], c["dtype"], c["R"]
+    print(f"[sweep-large] case {i}: {c}", flush=True)
+    g = torch.Generator().manual_seed(300 + i)
+    lin = torch.nn.Linear(K, N, bias=c["bias"])
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(N, K, generator=g) * 0.02)
+        if c["bias"]:
+            lin.bias.copy_(torch.randn(N, generator=g) * 0.01)
+    lr = None
+    if R:
+        lr = ((torch.randn(K, R, generator=g) * 0.02).to(dt), (torch.randn(R, N, generator=g) * 0.02).to(dt))
+    q = E.Int8Linear(lin, device=cuda, lowrank=lr, group_size=c["group"])
+    qo, so = oracle.quant_weight(lin.weight.detach().numpy(), c["group"])
+    assert np.array_equal(q.weight_int8.cpu().numpy(), qo)
+    assert np.array_equal(q.w_scale.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+    rows = M + 50 if c["routed"] else M
+    xf = torch.randn(rows, K + c["pad"], generator=g)
+    xf[:, torch.randperm(K, generator=g)[: max(1, K // 200)]] *= 20.0
+    x = xf.to(dt).to(cuda)[:, :K]
+    sample = torch.cat([torch.randperm(M - 40, generator=g)[:64], torch.arange(M - 40, M)]).sort().values
+    if c["routed"]:
+        ri = torch.randperm(rows, generator=g)[:M].to(torch.int32)
+        ori = torch.randperm(M + 30, generator=g)[:M].to(torch.int32)
+        canvas = torch.randn(M + 30, N, generator=g).to(dt).to(cuda)
+        before = canvas.clone()
+        q(x, row_idx=ri.to(cuda), out=canvas, out_row_idx=ori.to(cuda))
+        src, dst = ri[sample].long(), ori[sample].long()
+        y_rows = canvas[dst.to(cuda)]
+    else:
+        y = q(x)
+        assert y.dtype == dt and y.shape == (M, N)
+        src = sample
+        y_rows = y[sample.to(cuda)]
+    o = oracle.linear(bits(x[src.to(cuda)].contiguous()), dcode(dt), qo, so,
+                      None if q.bias is None else q.bias.cpu().numpy(), c["group"],
+                      None if lr is None else bits(lr[0]), None if lr is None else bits(lr[1]))
+    got = bits(y_rows)
+    if not R:
+        assert np.array_equal(got, o["out"]), "outputs without a low-rank branch must be bit-exact"
+    else:
+        yf = oracle.to_f32(got, dcode(dt))
+        mx, mean = rel_errors(yf, o["y"])
+        assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+        v = elem_violation(yf, o["y"], oracle.to_f32(o["t"], dcode(dt)), oracle.to_f32(bits(lr[1]), dcode(dt)))
+        assert v <= 1.0, v
+    if c["routed"]:
+        keep = torch.ones(M + 30, dtype=torch.bool)
+        keep[ori.long()] = False
+        assert torch.equal(canvas[keep.to(cuda)], before[keep.to(cuda)])
