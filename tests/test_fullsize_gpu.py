@@ -9,7 +9,8 @@ possibly ragged, tiles) and computes those rows on the CPU with the oracle from 
 * without a low-rank branch (c3), the 16-bit outputs bit-exact;
 * with one, the normwise bar (max 1e-2, mean 5e-3) and the element-wise bar of conftest.elem_violation.
 The routed case (c4) runs on the full 65536-row canvas: the routed rows land where the gather list says, every other
-row of the canvas is left as it was.
+row of the canvas is left as it was. A last case runs c1 at batch 2 (131584 rows), whose output rows lie past 2 GiB
+of byte offset.
 """
 import numpy as np
 import pytest
@@ -107,3 +108,26 @@ def test_routed_full_canvas(oracle, cuda):
     keep = torch.ones(c.M, dtype=torch.bool, device=cuda)
     keep[ri.long()] = False
     assert torch.equal(canvas[keep], before[keep]), "rows outside the gather list must keep the cached canvas"
+
+
+def test_layer_output_beyond_2gib(oracle, cuda):
+    """FLUX's 4K stage at batch 2 (M = 131584 tokens, the c1 layer): the 3.2 GB bf16 output and the 404 MB of codes
+    put rows past 2 GiB of byte offset (output rows from 87382 on), so every row address must be a 64-bit
+    product. 64 sampled rows past that point, the last 40 included, against the oracle."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import CONFIGS, make_linear, make_x
+
+    c = CONFIGS["c1"]
+    M = 2 * (c.M + 256)
+    print(f"[fullsize] c1 at batch 2: M={M} K={c.K} N={c.N}", flush=True)
+    q = E.Int8Linear(make_linear(c.K, c.N, c.lowrank, c.bias, dtype=c.dtype), device=cuda)
+    x = make_x(M, c.K, c.dtype, seed=11, device=cuda)
+    y = q(x)
+    assert y.shape == (M, c.N)
+    first = (1 << 31) // (c.N * 2) + 1                      # the first output row wholly past 2 GiB
+    g = torch.Generator().manual_seed(12)
+    rows = torch.cat([first + torch.randperm(M - 40 - first, generator=g)[:24], torch.arange(M - 40, M)])
+    rows = rows.sort().values
+    xq, sx, _ = _first_stage(E, q, x)
+    rd = rows.to(cuda)
+    _check_rows(oracle, q, bits(x[rd]), dcode(c.dtype), y[rd], _packed_rows(xq, rows, c.K), sx[rd].cpu().numpy())
