@@ -151,7 +151,7 @@ def test_int8linear_packed_path(oracle, cuda, cfg, M):
     assert torch.equal(y, ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(8191, 6464, 1280), (16400, 4160, 192)])
+@pytest.mark.parametrize("M,N,K", [(8191, 6464, 1280), (16400, 4160, 192), (16400, 4160, 64)])
 def test_gemm_big_tile_path_ragged(oracle, cuda, M, N, K):
     """Shapes with >= 1024 tiles of 256 x 128 take the 256 x 256 block of 8 waves; ragged M and N (tail tiles on
     both edges) stay exact there, row-major and packed, and the fused outputs agree bit for bit."""
@@ -237,11 +237,12 @@ def test_gemm_packed_group32_lowrank_scatter(oracle, cuda, lr):
 
 
 @pytest.mark.parametrize("M,N,K,lr", [(4352, 3072, 3072, 32), (4100, 3008, 1280, 0), (3000, 3072, 12288, 32),
-                                      (4096, 4096, 512, 0)])
+                                      (4096, 4096, 512, 0), (4096, 3072, 64, 0), (4100, 3008, 128, 32)])
 def test_gemm_one_round_big_tiles(oracle, cuda, M, N, K, lr):
     """Problems whose 256 x 256 blocks all fit in one round on the chip (at most one per CU) while their 128 x 128
     blocks would need more than one round take the 256 x 256 block (M = 4352 is FLUX's 1K token count; 4096 x 4096
-    is exactly one block per CU; the others are ragged in M and N, and long in K). The int32 accumulators are exact against the oracle on sampled rows, the
+    is exactly one block per CU; the others are ragged in M and N, long in K, or a single 64-wide K stage against
+    the ring's five). The int32 accumulators are exact against the oracle on sampled rows, the
     last ragged ones included, row-major and packed. The fused output is bit-identical to the same product computed
     in 256-row slices, whose few blocks run the 128 x 64 kernel with the same per-element epilogue arithmetic."""
     from pyraquant_amd import int8_exec as E
