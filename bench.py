@@ -11,7 +11,8 @@ of the whole layer). `roofline` prices the dominant kernel (the fused GEMM) agai
 `cpu_baseline` times the reference's torch CPU quantize + int-matmul path (restated in oracle/torch_ref.py) on
 a bounded row sample of the same layer.
 
-    python bench.py [--steps K] [--warmup W] [--config c1|c0|c2a|c2b|c3_1280|c3_5120|c4] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config c1|c0|c2a|c2b|c3_1280|c3_5120|c3_1280_f16|c3_5120_f16|c4]
+                    [--no-cpu] [--no-side] [--blaslt | --gemm-data | --copy-probe BYTES]
 """
 from __future__ import annotations
 
@@ -41,17 +42,12 @@ def main() -> int:
     ap.add_argument("--no-side", action="store_true",
                     help="skip the side measurements (routing kernels, SDXL small-M launches, weight fold), e.g. for "
                          "profiler runs that should hold the layer's kernels only")
+    ap.add_argument("--gemm-data", action="store_true",
+                    help="only time the layer's fused GEMM at the config's shape on the workload's own int8 codes and on "
+                         "synthetic operand bytes (uniform random, constant, zero), interleaved, and print one JSON line")
     ap.add_argument("--blaslt", action="store_true",
                     help="only compare the int32-output GEMM with hipBLASLt's (torch._int_mm) on the config's "
                          "operands, like for like, and print one JSON line")
-    ap.add_argument("--read-probe", action="store_true",
-                    help="only time streaming re-reads of buffers from 16 MB to 2 GB (plain and non-temporal loads): "
-                         "where the 256 MB memory-side cache serves a second read; one JSON line")
-    ap.add_argument("--mfma-ceiling", action="store_true",
-                    help="only run the register-only MFMA throughput probe (random / constant / zero operands, int8 "
-                         "and fp16 MFMA) and print one JSON line")
-    ap.add_argument("--mfma-kinds", type=str, default=None,
-                    help="with --mfma-ceiling: comma-separated probe loops to run (0-11; default all)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the INT8 executor "
@@ -76,16 +72,12 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": src.numel() * 4}), flush=True)
         return 0
-    if args.mfma_ceiling:
-        kinds = None if args.mfma_kinds is None else {int(k) for k in args.mfma_kinds.split(",")}
-        print(json.dumps(mfma_ceiling(dev, kinds)), flush=True)
-        return 0
-    if args.read_probe:
-        print(json.dumps(read_probe(dev)), flush=True)
-        return 0
     cfg = CONFIGS[args.config]
     if args.blaslt:
         print(json.dumps(blaslt_compare(dev, cfg)), flush=True)
+        return 0
+    if args.gemm_data:
+        print(json.dumps(gemm_data(dev, cfg)), flush=True)
         return 0
     lin = make_linear(cfg.K, cfg.N, cfg.lowrank, cfg.bias, dtype=cfg.dtype)
     q = E.Int8Linear(lin, device=dev, group_size=cfg.group)
@@ -287,116 +279,65 @@ def blaslt_compare(dev, cfg):
     return {"blaslt_compare": res, "int32_equal_to_int_mm": same, "config": cfg.name, "M": cfg.M, "K": cfg.K, "N": cfg.N}
 
 
-def read_probe(dev):
-    """Streaming reads (pyraquant_amd/csrc/probe/mfma_ceiling.hip, pq_probe_read) of one buffer of S bytes, read 6
-    times back to back, each read timed by HIP events: the first read comes from HBM, the later ones from the memory-side
-    cache when S fits it. Plain and non-temporal loads; 2048 workgroups of 256 threads."""
-    import ctypes
-
+def gemm_data(dev, cfg):
+    """The layer's fused GEMM (packed operands, dequant + low-rank + bias epilogue, bf16 out) at the config's shape on
+    four operand sets with the same scales, bias, t and lr_B: the workload's own codes (the config's x quantized by
+    the layer's quantizer, its weights by the layer's RTN), uniform random codes in [-127, 127], a constant 90, and
+    zeros. The MFMA's power draw, and so the clock it runs at, depends on the operand bits; the time on constant or
+    zero operands is the same kernel with that dependence taken out. 2 warm-up calls each, then 10 rounds interleaved
+    over the sets, each call timed by its own HIP event pair on the launch stream; medians."""
     import torch
 
-    from pyraquant_amd import build as B
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
 
-    lib = ctypes.CDLL(B.PROBE_PATH)
-    lib.pq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                  ctypes.c_void_p]
-    lib.pq_probe_read.restype = ctypes.c_int
+    q = E.Int8Linear(make_linear(cfg.K, cfg.N, cfg.lowrank, cfg.bias, dtype=cfg.dtype), device=dev,
+                     group_size=cfg.group)
+    x = make_x(cfg.M, cfg.K, cfg.dtype).to(dev)
+    if q.lr_At is not None:
+        xp, sx, t = E.quant_rows_lowrank(x, q.lr_At, None, q._lr_frag())
+    else:
+        (xp, sx), t = E.quant_rows_packed(x), None
+    del x
+    wp = q.weight_packed
+    g = torch.Generator(device=dev).manual_seed(5)
+    sets = {"workload": (xp, wp)}
+    for name, fill in (("random", None), ("constant", 90), ("zero", 0)):
+        if fill is None:
+            a = torch.randint(-127, 128, (cfg.M, cfg.K), generator=g, device=dev, dtype=torch.int8)
+            w = torch.randint(-127, 128, (cfg.N, cfg.K), generator=g, device=dev, dtype=torch.int8)
+        else:
+            a = torch.full((cfg.M, cfg.K), fill, device=dev, dtype=torch.int8)
+            w = torch.full((cfg.N, cfg.K), fill, device=dev, dtype=torch.int8)
+        sets[name] = (E.pack_k64(a), E.pack_k64(w))
+        del a, w
+    out = torch.empty(cfg.M, cfg.N, dtype=cfg.dtype, device=dev)
+
+    def call(ap, wq):
+        E.int8_gemm_packed(ap, sx, wq, q._scale_k(), q.bias, cfg.M, cfg.N, cfg.K, cfg.dtype, t=t, l2t=q.lr_Bt, out=out,
+                           group=q.group_size)
+
+    for ap, wq in sets.values():
+        call(ap, wq)
+        call(ap, wq)
+    torch.cuda.synchronize()
+    times = {k: [] for k in sets}
     stream = torch.cuda.current_stream(dev)
-    blocks = 2048
-    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
-    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)   # 1 GiB written between sizes: evicts the cache
-    cases = []
-    for mb in (16, 64, 128, 192, 256, 384, 512, 2048):
-        buf = torch.ones(mb << 20, dtype=torch.uint8, device=dev)
-        for nt in (0, 1):
-            flush.fill_(nt + 1)
-            gbs = []
-            for _ in range(6):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                assert lib.pq_probe_read(ctypes.c_void_p(buf.data_ptr()), buf.numel(), nt, blocks,
-                                         ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream.cuda_stream)) == 0
-                e1.record(stream)
-                torch.cuda.synchronize()
-                gbs.append(buf.numel() / (e0.elapsed_time(e1) * 1e-3) / 1e9)
-            cases.append({"MB": mb, "loads": "nontemporal" if nt else "plain", "first_GBps": round(gbs[0], 1),
-                          "reread_GBps_median": round(sorted(gbs[1:])[2], 1)})
-            print(f"[read-probe] {mb:5d} MB {'nt   ' if nt else 'plain'}: first {gbs[0]:8.1f} GB/s, "
-                  f"re-read {sorted(gbs[1:])[2]:8.1f} GB/s", flush=True)
-        del buf
-    return {"read_probe": cases}
-
-
-def mfma_ceiling(dev, kinds=None):
-    """Register-only MFMA loops (pyraquant_amd/csrc/probe/mfma_ceiling.hip) over the whole chip: the throughput the
-    matrix cores sustain with no memory traffic at all, for random, constant and zero operands, at 1, 2 and 4 waves
-    per SIMD. int8: v_mfma_i32_32x32x32_i8 against 5.0 POP/s; fp16: v_mfma_f32_32x32x16_f16 on the fp16 images of
-    int8 codes against 2.5 PFLOP/s; int8 again in 8-wave workgroups, with and without a static issue priority for
-    waves 0-3; and the group-32 inner loop (int8 MFMA + convert + fma against two fp16 MFMAs + fma, int8-equivalent
-    ops), plain and with the priority split. Each case: one warm-up launch, then the median of 3 launches timed by HIP events
-    on the launch stream (about 20 ms each)."""
-    import ctypes
-
-    import torch
-
-    from pyraquant_amd import build as B
-
-    lib = ctypes.CDLL(B.PROBE_PATH)
-    lib.pq_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                  ctypes.c_void_p]
-    lib.pq_probe_mfma.restype = ctypes.c_int
-    g = torch.Generator().manual_seed(7)
-    codes = {"random": torch.randint(-127, 128, (16 * 64 * 16,), generator=g, dtype=torch.int32),
-             "constant": torch.full((16 * 64 * 16,), 90, dtype=torch.int32),
-             "zero": torch.zeros(16 * 64 * 16, dtype=torch.int32)}
-    stream = torch.cuda.current_stream(dev)
-    sink = torch.empty(256 * 4 * 256, dtype=torch.int32, device=dev)
-    cases = []
-    # (kind, MFMA, ops per instruction, peak, waves per workgroup, operand patterns, waves per SIMD)
-    plan = ((0, "i32_32x32x32_i8", 65536, INT8_PEAK_TOPS, 4, ("random", "constant", "zero"), (1, 2, 4)),
-            (1, "f32_32x32x16_f16", 32768, INT8_PEAK_TOPS / 2, 4, ("random", "constant", "zero"), (1, 2, 4)),
-            (2, "i32_32x32x32_i8 8-wave WG", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)),
-            (3, "i32_32x32x32_i8 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8, ("random", "constant"), (2, 4)),
-            (4, "group-32 loop: i8 MFMA + cvt + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2, 4)),
-            (5, "group-32 loop: 2 f16 MFMA + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2, 4)),
-            (6, "group-32 loop: i8 MFMA + cvt + fma, 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8,
-             ("random",), (2, 4)),
-            (7, "group-32 loop: 2 f16 MFMA + fma, 8-wave WG, waves 0-3 prio 1", 65536, INT8_PEAK_TOPS, 8, ("random",),
-             (2, 4)),
-            (8, "group-32 loop, pipelined: 2 f16 MFMA + fma", 65536, INT8_PEAK_TOPS, 4, ("random", "constant"), (1, 2)),
-            (9, "group-32 loop, pipelined: i8 MFMA + cvt + fma", 65536, INT8_PEAK_TOPS, 4, ("random",), (1, 2)),
-            (10, "group-32 loop, pipelined: i8 MFMA from 1.5*2^23 + sub + fma", 65536, INT8_PEAK_TOPS, 4, ("random",),
-             (1, 2)),
-            (11, "group-32 loop, pipelined: i8 MFMA + fma only (timing reference)", 65536, INT8_PEAK_TOPS, 4,
-             ("random",), (1, 2)))
-    if kinds is not None:
-        plan = tuple(row for row in plan if row[0] in kinds)
-    for kind, name, per_inst, peak, wpb, patterns, wps_list in plan:
-        for pattern in patterns:
-            c = codes[pattern]
-            # int8: the bytes themselves; fp16: 8 codes per 16-byte fragment as fp16 values (exact)
-            src = (c[: 16 * 64 * 16].to(torch.int8) if kind not in (1, 5, 7, 8) else c[: 16 * 64 * 8].to(torch.float16)).to(dev)
-            for wps in wps_list:
-                blocks, iters = 256 * wps * 4 // wpb, 100000 // wps
-                call = lambda: lib.pq_probe_mfma(kind, ctypes.c_void_p(src.data_ptr()), blocks, iters,
-                                                 ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream.cuda_stream))
-                assert call() == 0, "probe launch failed"
-                ms = []
-                for _ in range(3):
-                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    e0.record(stream)
-                    call()
-                    e1.record(stream)
-                    torch.cuda.synchronize()
-                    ms.append(e0.elapsed_time(e1))
-                t = sorted(ms)[1] * 1e-3
-                ops = float(blocks) * wpb * iters * 8 * per_inst   # kinds 4, 5: 2 groups x 4 tiles per iteration
-                rate = ops / t / 1e12
-                cases.append({"mfma": name, "operands": pattern, "waves_per_simd": wps, "ms": round(t * 1e3, 3),
-                              "TOPS": round(rate, 1), "frac_of_peak": round(rate / peak, 4)})
-                print(f"[mfma-ceiling] {name} {pattern:8s} {wps} waves/SIMD: {rate:8.1f} TOP/s "
-                      f"({100 * rate / peak:5.1f} % of {peak:.0f})", flush=True)
-    return {"mfma_ceiling": cases, "gpu": torch.cuda.get_device_name(dev)}
+    for _ in range(10):
+        for k, (ap, wq) in sets.items():
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            call(ap, wq)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times[k].append(e0.elapsed_time(e1) * 1e3)
+    ops = 2.0 * cfg.M * cfg.N * cfg.K
+    res = {}
+    for k, v in times.items():
+        us = sorted(v)[len(v) // 2]
+        res[k] = {"us": round(us, 1), "TOPS": round(ops / us / 1e6, 1),
+                  "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)}
+    return {"gemm_data": res, "order": list(sets), "config": cfg.name, "M": cfg.M, "K": cfg.K, "N": cfg.N}
 
 
 def fold_bench(dev, cfg):

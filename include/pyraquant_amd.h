@@ -3,11 +3,14 @@
  *
  * The library replaces the GPU kernels behind PyraQuant's `Int8Linear` executor
  * (reference: deploy/int8_exec.py, deploy/run_sdxl_latency.py). Every entry point takes raw device
- * pointers, element strides and a HIP stream; nothing here allocates or frees device memory, and no
- * entry point synchronises the stream. All calls are asynchronous on `stream` (pass the caller's
- * current stream; torch: torch.cuda.current_stream().cuda_stream). The C API keeps no mutable global
- * state apart from the thread-local error text and pq_int8_linear_noalloc's device array (one per GPU,
- * see there), so every other entry point may be called from several host threads.
+ * pointers, element strides and a HIP stream; no entry point allocates, frees or clears device memory with a
+ * runtime call (hipMalloc, hipFree, hipMemset*), and none synchronises the stream. All calls are asynchronous
+ * on `stream` (pass the caller's current stream; torch: torch.cuda.current_stream().cuda_stream). Memory the
+ * kernels use beyond their inputs and outputs is the caller's: the GEMMs' optional scheduling buffer (`sched`)
+ * and pq_int8_linear's workspace. The one exception is pq_int8_linear_noalloc's staging, a 64 MiB static device
+ * array that the HIP runtime maps on every GPU the library's code object is loaded on, whether or not that
+ * entry point is ever called. The C API keeps no other mutable global state apart from the thread-local error
+ * text, so every entry point other than pq_int8_linear_noalloc may be called from several host threads.
  *
  * Return value of every int-returning entry point: PQ_OK (0) or a negative PQ_E* code; the text of the
  * last error on the calling thread is available from pq_last_error().
@@ -42,7 +45,7 @@
 extern "C" {
 #endif
 
-#define PQ_ABI_VERSION 2
+#define PQ_ABI_VERSION 3
 
 /* status codes */
 #define PQ_OK 0
@@ -129,18 +132,19 @@ int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t K, int64_t 
  * c 8-byte aligned with ldc % 4 == 0 and ldc < 2^31; t, l2t 16-byte aligned with ldt % 8 == 0, ldt <= 2^22,
  * R in {16, 32, 64}; group 32 needs N * K < 2^33 (its scales are read at 32-bit buffer offsets);
  * lr_dtype and out_dtype are PQ_BF16 or PQ_F16; out_row_idx entries unique (two rows naming one row of c race).
- * Large products (rank 0-32, no accumulate, more 256 x 256 blocks than CUs) run one persistent workgroup per CU
- * that claims blocks from per-XCD counters in a 36-byte buffer on the stream's device, belonging to the stream:
- * the library allocates it on the first such launch on that stream (never while the stream is being
- * captured, and in relaxed capture mode), and each launch leaves it zeroed for the next. Launches on different
- * streams never share one. A stream being captured gets a fixed share of blocks per workgroup instead, as does
- * pq_int8_linear_noalloc, so a graph replays without the buffer. The results do not depend on the schedule.
+ * sched: NULL, or a scheduling buffer of 9 int32 (36 bytes, 4-byte aligned) on the stream's device that the
+ * caller owns. Large products (rank 0-32, no accumulate, more 256 x 256 blocks than CUs) run one persistent
+ * workgroup per CU. With a buffer, the workgroups claim blocks from per-XCD counters in it, so the faster XCDs take
+ * the slower ones' last blocks; without one, each takes a fixed share. The buffer must hold zeros when the launch
+ * starts (e.g. torch.zeros once), and every launch leaves it zeroed, so launches ordered on one stream may share it
+ * and launches that may overlap (other streams, a graph replayed beside eager work) must not. Smaller products
+ * ignore it. The results do not depend on the schedule.
  */
 int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64_t ldw,
                  const float* s_row, const float* s_w, int64_t group, const float* bias,
                  const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
                  void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows,
-                 int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                 int64_t M, int64_t N, int64_t K, int32_t* sched, hipStream_t stream);
 
 /*
  * int32 accumulator only: c[m, n] = sum_k a[m, k] * w[n, k] (exact). The bit-exact check of the
@@ -184,19 +188,20 @@ int pq_pack_lowrank_l1t(const void* l1t, int32_t dtype, int64_t R, int64_t K, vo
  * output, group 0), each output element is added to what c holds: c = round(c + round(y)), so a Linear split along
  * its input accumulates its second half into the first half's output in the same pass that writes it
  * (`SplitInLinear.forward`'s `L0(x0) + L1(x1)`, pyraquant/external_quant.py:191-192). This is the layer path of Int8Linear: the quantizer writes ap directly
- * (pq_quant_rows_packed) and the weights are packed once at conversion (pq_pack_k64). Large products run persistent
- * workgroups with the stream's scheduling buffer, as pq_int8_gemm describes.
+ * (pq_quant_rows_packed) and the weights are packed once at conversion (pq_pack_k64). sched as pq_int8_gemm
+ * describes (ignored with PQ_I32 or PQ_ACCUMULATE).
  * Replaces `int8_gemm_fused` / `int8_gemm_lr` (deploy/int8_exec.py:202-212, 327-336) as called from
  * `Int8Linear.forward` (deploy/int8_exec.py:382-393).
  */
 int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w, int64_t group,
                         const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
                         void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows,
-                        int64_t M, int64_t N, int64_t K, hipStream_t stream);
+                        int64_t M, int64_t N, int64_t K, int32_t* sched, hipStream_t stream);
 
 /*
  * Bytes of workspace pq_int8_linear needs for M rows, K inputs and R columns of t (R = 0: no low-rank branch):
- * the packed codes, the row scales and t, each slice starting on a 256-byte boundary. -1 for a bad argument.
+ * the packed codes, the row scales, t and the GEMM's 36-byte scheduling buffer, each slice starting on a 256-byte
+ * boundary. -1 for a bad argument.
  * No reference counterpart (the reference allocates the three tensors per call with torch.empty,
  * deploy/int8_exec.py:225-226, 390).
  */
@@ -210,8 +215,9 @@ int64_t pq_int8_linear_workspace_size(int64_t M, int64_t K, int64_t R);
  * weights [N, K]; s_w [N] (group 0) or [K/32, N] (group 32); bias [N] fp32 or NULL; l1t [R, K] and l2t [N, Re] in
  * x's dtype (R a multiple of 32 up to 128, Re in {16, 32, 64} and Re <= R: the first Re columns of t enter the
  * epilogue), or NULL with R = Re = 0; l1f NULL or l1t in fragment order (as pq_quant_rows_lowrank); y [M, N] in
- * x's dtype with row stride ldy. Same results as the two calls. Its GEMM uses the stream's scheduling buffer as
- * pq_int8_gemm describes (allocated once per stream, outside the workspace).
+ * x's dtype with row stride ldy. Same results as the two calls. The workspace also holds the GEMM's scheduling
+ * buffer (pq_int8_gemm's sched), which the quantizer kernel zeroes, so a large layer claims its blocks even when
+ * replayed from a graph; calls that may overlap need workspaces of their own.
  * Replaces the body of `Int8Linear.forward` (deploy/int8_exec.py:382-393): one C call per layer.
  */
 int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
@@ -220,14 +226,15 @@ int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t
                    hipStream_t stream);
 
 /*
- * pq_int8_linear without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference, which
- * allocates its intermediates with torch per call (deploy/int8_exec.py:225-226, 390). The staging lives in a device
- * array of the library, pq_int8_linear_noalloc_max_bytes() bytes (64 MiB) on each GPU it runs on, held until the
- * process ends; a layer whose pq_int8_linear_workspace_size(M, K, R) exceeds that is refused with PQ_ESHAPE before
- * any work (FLUX's 1K-stage and SDXL's layers fit; FLUX's 4K stage does not). Nothing is allocated, freed or
- * cleared per call. `stream` must belong to the current device. Every call on a GPU uses that GPU's one array:
- * calls that overlap on one GPU (other streams, other threads) race, so serialise them. Arguments and results as
+ * pq_int8_linear without a workspace argument. No counterpart in the reference; it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The workspace (codes, scales, t and the scheduling buffer) lives in a static device array of the library,
+ * pq_int8_linear_noalloc_max_bytes() bytes (64 MiB). The runtime maps that array on every GPU the library's code
+ * object is loaded on, whether or not this entry point is called, and holds it until the process ends. A layer
+ * whose pq_int8_linear_workspace_size(M, K, R) exceeds it is refused with PQ_ESHAPE before any work (FLUX's
+ * 1K-stage and SDXL's layers fit; FLUX's 4K stage does not). Nothing is allocated or freed per call. `stream` must
+ * belong to the current device. Every call on a GPU uses that GPU's one array: calls that overlap on one GPU
+ * (other streams, other threads) race, so serialise them. The other arguments and the result are those of
  * pq_int8_linear.
  */
 int pq_int8_linear_noalloc(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,

@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpqint8.s
 PQ_OK, PQ_EINVAL, PQ_ESHAPE, PQ_EALIGN, PQ_EDTYPE, PQ_ELAUNCH = 0, -1, -2, -3, -4, -5
 PQ_BF16, PQ_F16, PQ_I32 = 0, 1, 2
 PQ_ACCUMULATE = 0x100   # OR'ed into pq_int8_gemm_packed's out_dtype
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # every entry point declared in include/pyraquant_amd.h
 EXPORTS = (
@@ -56,10 +56,10 @@ _SIGNATURES = {
     "pq_quant_weight": ([_p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "pq_lowrank_down": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p], ctypes.c_int),
     "pq_int8_gemm": ([_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p, _i64,
-                      _i64, _i64, _i64, _p], ctypes.c_int),
+                      _i64, _i64, _i64, _p, _p], ctypes.c_int),
     "pq_int8_gemm_i32": ([_p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _p], ctypes.c_int),
     "pq_int8_gemm_packed": ([_p, _p, _p, _p, _i64, _p, _p, _i64, _p, _i64, _i32, _p, _i64, _i32, _p, _i64, _i64, _i64,
-                             _i64, _p],
+                             _i64, _p, _p],
                             ctypes.c_int),
     "pq_pack_k64": ([_p, _i64, _i64, _i64, _p, _p], ctypes.c_int),
     "pq_quant_rows_packed": ([_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),

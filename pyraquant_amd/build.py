@@ -117,23 +117,7 @@ def build(verbose: bool = False) -> str:
         if r.returncode != 0:
             raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
         os.replace(out_tmp, LIB_PATH)
-    build_probe()
     return LIB_PATH
-
-
-PROBE_SRC = os.path.join(CSRC, "probe", "mfma_ceiling.hip")
-PROBE_PATH = os.path.join(HERE, "libpqprobe.so")
-
-
-def build_probe() -> str:
-    """The register-only MFMA throughput probe (`bench.py --mfma-ceiling`), a library of its own: it measures the
-    chip, it is not part of the executor's ABI."""
-    cmd = [_hipcc(), *HIP_FLAGS, "-shared", PROBE_SRC, "-o", PROBE_PATH + ".tmp"]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on {PROBE_SRC}:\n{r.stdout}{r.stderr}")
-    os.replace(PROBE_PATH + ".tmp", PROBE_PATH)
-    return PROBE_PATH
 
 
 if __name__ == "__main__":

@@ -15,12 +15,20 @@ int check_launch(const char* what);
 // A dispatch counts work-items in 32 bits per dimension: blocks * threads must stay below 2^32.
 int check_grid(int64_t blocks, int64_t threads, const char* what);
 
-// pq_int8_gemm_packed with the choice of whether a large GEMM may allocate its stream's scheduling buffer
-// (pq_gemm.hip); the allocation-free layer call passes false.
+// pq_int8_gemm_packed (pq_gemm.hip), called by the layer entries with a scheduling buffer in their staging.
 int int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w, int64_t group,
                      const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
                      void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows, int64_t M,
-                     int64_t N, int64_t K, hipStream_t stream, bool sched_alloc);
+                     int64_t N, int64_t K, int32_t* sched, hipStream_t stream);
+
+// pq_quant_rows_packed / pq_quant_rows_lowrank (pq_quant.hip) that also write zeros to zero9[0 .. 8] (when not NULL)
+// in the same kernel: the layer entries clear their GEMM's scheduling buffer this way, with no memset and no extra
+// launch (a captured graph clears it on every replay).
+int quant_rows_packed_z(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
+                        const int32_t* row_idx, int8_t* qp, float* s, int32_t* zero9, hipStream_t stream);
+int quant_rows_lowrank_z(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
+                         const int32_t* row_idx, const void* l1t, const void* l1f, int64_t R, int8_t* qp, float* s,
+                         void* t, int64_t ldt, int32_t* zero9, hipStream_t stream);
 
 // ---- vector types of the MFMA operands -----------------------------------------------------------------
 typedef int v4i __attribute__((ext_vector_type(4)));

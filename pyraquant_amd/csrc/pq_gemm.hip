@@ -32,14 +32,12 @@
 //
 // Workgroup ids are remapped so that each XCD (ids are dealt round-robin over the 8 XCDs) walks a contiguous
 // run of tiles, rasterised in groups of group_m() m-tiles for L2 reuse. Large 256 x 256 products run one persistent
-// workgroup per CU, which claims its XCD's tiles (then the other XCDs') through a per-stream scheduling buffer.
+// workgroup per CU, which claims its XCD's tiles (then the other XCDs') through a scheduling buffer the caller owns
+// (or, without one, takes a fixed share of them).
 #include "pq_common.h"
 
 #include <atomic>
-#include <map>
-#include <mutex>
 #include <type_traits>
-#include <utility>
 
 namespace pq {
 namespace {
@@ -65,7 +63,6 @@ struct GemmArgs {
   int M, N, K, R;
   int tiles_m, tiles_n;
   int* sched;         // persistent blocks: 9 ints of claim counters, zero at launch and left zero (or NULL)
-  bool sched_alloc;   // host side: the entry may allocate a scheduling buffer for the stream (not noalloc)
 };
 
 enum { kModeI32 = 0, kModeChannel = 1, kModeGroup32 = 2 };
@@ -529,13 +526,25 @@ void gemm_dma_kernel(const GemmArgs p) {
   // up to 165 us apart at c1. Without the buffer it steps vb by the grid size (a fixed share per workgroup).
   constexpr bool PERSIST = persistent_block<TI, TJ, WMW, NS, OCC, MODE, LRS, LRDT, ODT, ACC>();
   const int nbt = p.tiles_m * p.tiles_n;
-  auto claim = [&](int vb) -> int {   // the virtual block after vb
+  // Claims (lane 0 of wave 0). XCD x's list holds cnt(x) tiles, of which first(x) went out as first tiles.
+  const int x0 = blockIdx.x & 7;
+  auto xcd_cnt = [&](int x) { return (nbt >> 3) + (x < (nbt & 7) ? 1 : 0); };
+  auto xcd_first = [&](int x) { return ((int)gridDim.x - x + 7) >> 3; };
+  // Part 1, issued before the epilogue so that the atomic's round trip overlaps it: the next local index of the own
+  // XCD's list (or cnt(x0) if the first tiles took them all).
+  auto claim_own = [&]() -> int {
+    if (xcd_first(x0) >= xcd_cnt(x0)) return xcd_cnt(x0);
+    return atomicAdd(p.sched + x0, 1) + xcd_first(x0);
+  };
+  // Part 2, after the epilogue: the own index if the list still had one, else the other 7 lists in a rotated order,
+  // so that stealers spread over the victims. Without a scheduling buffer, the fixed share: vb + grid.
+  auto claim_rest = [&](int vb, int own) -> int {
     if (!p.sched) return vb + (int)gridDim.x;
-    const int per = nbt >> 3, rem = nbt & 7, x0 = blockIdx.x & 7, rot = blockIdx.x >> 3;
-    for (int k = 0; k < 8; ++k) {
-      const int x = k == 0 ? x0 : (x0 + 1 + (k - 1 + rot) % 7) & 7;   // own list, then the other 7 in turn
-      const int cnt = per + (x < rem ? 1 : 0);                        // XCD x's tiles
-      const int first = ((int)gridDim.x - x + 7) >> 3;                // of them taken as first tiles
+    if (own < xcd_cnt(x0)) return (own << 3) | x0;
+    const int rot = blockIdx.x >> 3;
+    for (int k = 1; k < 8; ++k) {
+      const int x = (x0 + 1 + (k - 1 + rot) % 7) & 7;
+      const int cnt = xcd_cnt(x), first = xcd_first(x);
       if (first >= cnt) continue;
       const int li = atomicAdd(p.sched + x, 1) + first;
       if (li < cnt) return (li << 3) | x;
@@ -822,9 +831,9 @@ void gemm_dma_kernel(const GemmArgs p) {
   mm(f1, KT - 1, 1);
   wait_dma<0>();     // the epilogue operands, and the out-of-range DMAs of the last iterations, have landed
   __syncthreads();   // every wave is done reading the ring: it becomes the output staging area
-  // the next tile's claim goes out now and is used after the epilogue, which covers its latency
-  int next = nbt;
-  if (PERSIST && wave == 0 && lane == 0) next = claim(vb);
+  // the own-list claim of the next tile goes out now; its result is read after the epilogue, which covers its latency
+  int own = 0;
+  if (PERSIST && p.sched && wave == 0 && lane == 0) own = claim_own();
   if constexpr (ELDS) {
     // buffers of stages KT (rows) and KT + 1 (columns) hold the operands; staging in the NS - 2 others
     constexpr int kSpb = STAGE / Epi::kStageBytesL;
@@ -842,7 +851,7 @@ void gemm_dma_kernel(const GemmArgs p) {
     // only after the second barrier.
     static_assert(kRowSlots < NW * (DW + DA), "the row buffer's last slot holds no epilogue operand");
     int* const slot = reinterpret_cast<int*>(smem + (KT % NS) * STAGE + STAGE - 4);
-    if (wave == 0 && lane == 0) *slot = next;
+    if (wave == 0 && lane == 0) *slot = claim_rest(vb, own);
     lds_barrier();
     vb = *slot;
     lds_barrier();   // every wave has read it, and is done with the staging area, before the next tile's DMA
@@ -850,7 +859,7 @@ void gemm_dma_kernel(const GemmArgs p) {
     vb = nbt;
   }
   }
-  // The last workgroup out leaves the scheduling buffer as it found it (zero) for the next launch on its stream.
+  // The last workgroup out leaves the scheduling buffer as it found it (zero) for the caller's next launch.
   if (PERSIST && p.sched && wave == 0 && lane == 0) {
     if (atomicAdd(p.sched + 8, 1) == (int)gridDim.x - 1) {
 #pragma unroll
@@ -901,68 +910,20 @@ int persistent_workgroups(hipStream_t stream) {
   return cus;
 }
 
-// The scheduling buffer of a stream: 9 ints on the stream's device, zeroed once when first handed out (in the
-// stream's order) and left zero by every launch that uses it, so launches on one stream share it and launches on
-// different streams never do. NULL while the stream is being captured (a graph keeps the static schedule, so a
-// replay never shares a buffer with eager launches) or if the allocation fails. The allocation runs in relaxed
-// capture mode so that another thread's global-mode capture is not invalidated by it. At most 1024 buffers per
-// process; later streams get NULL.
-int* stream_sched(hipStream_t stream) {
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  if (cs != hipStreamCaptureStatusNone) return nullptr;
-  // the stream's device holds the buffer (the kernel runs there, whichever device is current)
-  int dev = -1, cur = -1;
-  if (hipStreamGetDevice(stream, &dev) != hipSuccess || hipGetDevice(&cur) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  static std::mutex mu;
-  static std::map<std::pair<int, hipStream_t>, int*> bufs;
-  std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair(dev, stream);
-  const auto it = bufs.find(key);
-  if (it != bufs.end()) return it->second;
-  if (bufs.size() >= 1024) return nullptr;
-  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
-  if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  int* buf = nullptr;
-  hipError_t e = dev == cur ? hipSuccess : hipSetDevice(dev);
-  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&buf), 9 * sizeof(int));
-  if (e == hipSuccess) e = hipMemsetAsync(buf, 0, 9 * sizeof(int), stream);
-  if (e != hipSuccess && buf) {
-    (void)hipFree(buf);
-    buf = nullptr;
-  }
-  if (dev != cur) (void)hipSetDevice(cur);
-  (void)hipThreadExchangeStreamCaptureMode(&mode);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    return nullptr;
-  }
-  bufs.emplace(key, buf);
-  return buf;
-}
-
 template <int TI, int TJ, int WMW, int OCC, bool PACKED, int MODE, int LRS, int LRDT, int ODT, bool ACC = false>
 int launch_dma(GemmArgs& a, hipStream_t stream) {
   constexpr int NS = ring_stages<TI, TJ, WMW, OCC, MODE>();
   dim3 grid;
   const int st = grid_of(a, 32 * TJ * WMW, 64 * TI, 128 * WMW, grid);
   if (st != PQ_OK) return st;
+  int* const sched = a.sched;   // the caller's scheduling buffer (or NULL): used by persistent launches only
   a.sched = nullptr;
   if constexpr (persistent_block<TI, TJ, WMW, NS, OCC, MODE, LRS, LRDT, ODT, ACC>()) {
     // one workgroup per CU; each XCD's share of workgroups claims that XCD's tiles (see the kernel)
     const int wg = persistent_workgroups(stream);
     if (wg > 0 && grid.x > (unsigned)wg) {
       grid.x = (unsigned)wg;
-      if (a.sched_alloc) a.sched = stream_sched(stream);
+      a.sched = sched;
     }
   }
   hipLaunchKernelGGL((gemm_dma_kernel<TI, TJ, WMW, NS, OCC, PACKED, MODE, LRS, LRDT, ODT, ACC>), grid, dim3(128 * WMW), 0,
@@ -1066,10 +1027,11 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
                             const float* s_w, int64_t group, const float* bias, const void* t, int64_t ldt,
                             const void* l2t, int64_t R, int32_t lr_dtype, void* c, int64_t ldc,
                             int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows, int64_t M, int64_t N,
-                            int64_t K, hipStream_t stream) {
+                            int64_t K, int32_t* sched, hipStream_t stream) {
   int st = check_common(a, lda, w, ldw, M, N, K, "pq_int8_gemm");
   if (st != PQ_OK) return st;
   if (M == 0) return PQ_OK;
+  if ((uintptr_t)sched % 4) return set_error(PQ_EALIGN, "pq_int8_gemm: sched must be 4-byte aligned");
   if (out_row_idx && c_rows < 1)
     return set_error(PQ_ESHAPE, "pq_int8_gemm: a scatter needs the rows of c (c_rows=%lld)", (long long)c_rows);
   if (!s_row || !s_w || !c) return set_error(PQ_EINVAL, "pq_int8_gemm: null s_row / s_w / c");
@@ -1097,7 +1059,7 @@ extern "C" int pq_int8_gemm(const int8_t* a, int64_t lda, const int8_t* w, int64
   args.c = c; args.out_row_idx = out_row_idx; args.c_rows = c_rows;
   args.lda = lda; args.ldw = ldw; args.ldt = ldt; args.ldc = ldc;
   args.M = (int)M; args.N = (int)N; args.K = (int)K; args.R = (int)R;
-  args.sched_alloc = true;
+  args.sched = sched;
   if (group == 32) return dispatch_dtypes<false, kModeGroup32>(args, has_lr, lr_dtype, out_dtype, stream);
   return dispatch_dtypes<false, kModeChannel>(args, has_lr, lr_dtype, out_dtype, stream);
 }
@@ -1122,7 +1084,7 @@ extern "C" int pq_int8_gemm_i32(const int8_t* a, int64_t lda, const int8_t* w, i
 int pq::int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row, const float* s_w, int64_t group,
                          const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R, int32_t lr_dtype,
                          void* c, int64_t ldc, int32_t out_dtype, const int32_t* out_row_idx, int64_t c_rows,
-                         int64_t M, int64_t N, int64_t K, hipStream_t stream, bool sched_alloc) {
+                         int64_t M, int64_t N, int64_t K, int32_t* sched, hipStream_t stream) {
   const bool accumulate = (out_dtype & PQ_ACCUMULATE) != 0;
   out_dtype &= ~PQ_ACCUMULATE;
   if (M < 0 || N < 1 || K < 1) return set_error(PQ_ESHAPE, "pq_int8_gemm_packed: bad shape");
@@ -1135,10 +1097,11 @@ int pq::int8_gemm_packed(const int8_t* ap, const int8_t* wp, const float* s_row,
   if (M == 0) return PQ_OK;
   if (!ap || !wp || !c) return set_error(PQ_EINVAL, "pq_int8_gemm_packed: null operand");
   if ((uintptr_t)ap % 16 || (uintptr_t)wp % 16) return set_error(PQ_EALIGN, "pq_int8_gemm_packed: ap / wp must be 16-byte aligned");
+  if ((uintptr_t)sched % 4) return set_error(PQ_EALIGN, "pq_int8_gemm_packed: sched must be 4-byte aligned");
   GemmArgs args{};
   args.a = ap; args.w = wp; args.c = c;
   args.M = (int)M; args.N = (int)N; args.K = (int)K;
-  args.sched_alloc = sched_alloc;
+  args.sched = sched;
   if (accumulate && (out_dtype == PQ_I32 || group != 0))
     return set_error(PQ_EINVAL, "pq_int8_gemm_packed: PQ_ACCUMULATE takes a 16-bit output and per-channel weights");
   if (out_dtype == PQ_I32) {
@@ -1184,7 +1147,7 @@ extern "C" int pq_int8_gemm_packed(const int8_t* ap, const int8_t* wp, const flo
                                    int64_t group, const float* bias, const void* t, int64_t ldt, const void* l2t, int64_t R,
                                    int32_t lr_dtype, void* c, int64_t ldc, int32_t out_dtype,
                                    const int32_t* out_row_idx, int64_t c_rows, int64_t M, int64_t N, int64_t K,
-                                   hipStream_t stream) {
+                                   int32_t* sched, hipStream_t stream) {
   return pq::int8_gemm_packed(ap, wp, s_row, s_w, group, bias, t, ldt, l2t, R, lr_dtype, c, ldc, out_dtype, out_row_idx,
-                              c_rows, M, N, K, stream, true);
+                              c_rows, M, N, K, sched, stream);
 }

@@ -6,8 +6,9 @@
 //   [0, QB)           packed K64 codes, QB = ceil(M / 16) * 16 * K bytes
 //   [SO, SO + 4 M)    fp32 row scales, SO = round256(QB)
 //   [TO, TO + 2 M R)  16-bit t [M, R], TO = SO + round256(4 M)
-// The quantizer writes every byte the GEMM reads (padding code rows included), so the workspace needs no clearing
-// and may hold anything on entry.
+//   [CO, CO + 36)     the GEMM's scheduling buffer (9 int32 claim counters), CO = TO + round256(2 M R)
+// The quantizer writes every byte the GEMM reads (padding code rows included) and zeroes the scheduling buffer in
+// the same kernel, so the workspace needs no clearing and may hold anything on entry.
 #include "pq_common.h"
 
 #include <mutex>
@@ -18,14 +19,17 @@ namespace {
 constexpr int64_t round256(int64_t b) { return (b + 255) & ~int64_t(255); }
 
 struct LayerSlices {
-  int64_t scales, t, total;
+  int64_t scales, t, sched, total;
 };
+
+constexpr int64_t kSchedBytes = 9 * sizeof(int32_t);
 
 LayerSlices layer_slices(int64_t M, int64_t K, int64_t R) {
   LayerSlices s;
   s.scales = round256(((M + 15) / 16) * 16 * K);
   s.t = s.scales + round256(4 * M);
-  s.total = s.t + 2 * M * R;
+  s.sched = s.t + round256(2 * M * R);
+  s.total = s.sched + kSchedBytes;
   return s;
 }
 
@@ -34,17 +38,17 @@ LayerSlices layer_slices(int64_t M, int64_t K, int64_t R) {
 // The layer over a workspace the caller provides (shared by pq_int8_linear and its allocation-free variant).
 static int run_layer(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w_packed,
                      const float* s_w, int64_t group, const float* bias, const void* l1t, const void* l1f, int64_t R,
-                     const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N, uint8_t* ws, hipStream_t stream,
-                     bool sched_alloc) {
+                     const void* l2t, int64_t Re, void* y, int64_t ldy, int64_t N, uint8_t* ws, hipStream_t stream) {
   const LayerSlices sl = layer_slices(M, K, R);
   int8_t* const q = reinterpret_cast<int8_t*>(ws);
   float* const s = reinterpret_cast<float*>(ws + sl.scales);
   void* const t = R ? static_cast<void*>(ws + sl.t) : nullptr;
-  int st = R ? pq_quant_rows_lowrank(x, x_dtype, M, K, ldx, M, nullptr, l1t, l1f, R, q, s, t, R, stream)
-             : pq_quant_rows_packed(x, x_dtype, M, K, ldx, M, nullptr, q, s, stream);
+  int32_t* const sched = reinterpret_cast<int32_t*>(ws + sl.sched);   // zeroed by the quantizer kernel
+  int st = R ? quant_rows_lowrank_z(x, x_dtype, M, K, ldx, M, nullptr, l1t, l1f, R, q, s, t, R, sched, stream)
+             : quant_rows_packed_z(x, x_dtype, M, K, ldx, M, nullptr, q, s, sched, stream);
   if (st != PQ_OK) return st;
   return int8_gemm_packed(q, w_packed, s, s_w, group, bias, R ? t : nullptr, R, R ? l2t : nullptr, Re, x_dtype, y, ldy,
-                          x_dtype, nullptr, 0, M, N, K, stream, sched_alloc);
+                          x_dtype, nullptr, 0, M, N, K, sched, stream);
 }
 
 int check_layer(int64_t M, int64_t K, int64_t N, int64_t R, int64_t Re, const void* l1t, const void* l2t,
@@ -80,7 +84,7 @@ extern "C" int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t
                      (long long)need);
   if ((uintptr_t)workspace % 256) return set_error(PQ_EALIGN, "pq_int8_linear: the workspace must be 256-byte aligned");
   return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, l1f, R, l2t, Re, y, ldy, N,
-                   static_cast<uint8_t*>(workspace), stream, true);
+                   static_cast<uint8_t*>(workspace), stream);
 }
 
 // ---- allocation-free variant -------------------------------------------------------------------------------------
@@ -89,7 +93,8 @@ extern "C" int pq_int8_linear(const void* x, int32_t x_dtype, int64_t M, int64_t
 // code `scratch` names a host-side stand-in, not the device array: its device address comes from
 // hipGetSymbolAddress, once per device (with that device current), and only that address is passed to kernels.
 // Every call on a GPU shares that GPU's array, so calls that overlap on one GPU (two streams, two threads) race.
-// Nothing here needs clearing: the quantizer writes every byte of the slices the GEMM reads.
+// Nothing here needs clearing: the quantizer writes every byte of the slices the GEMM reads, and zeroes the GEMM's
+// scheduling buffer (the array's workspace layout is pq_int8_linear's).
 constexpr int64_t kScratchBytes = 64LL << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -143,7 +148,5 @@ extern "C" int pq_int8_linear_noalloc(const void* x, int32_t x_dtype, int64_t M,
   uint8_t* ws = nullptr;
   st = device_scratch(stream, &ws);
   if (st != PQ_OK) return st;
-  // no scheduling buffer either: a large GEMM keeps the static schedule (nothing is allocated)
-  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, l1f, R, l2t, Re, y, ldy, N, ws, stream,
-                   false);
+  return run_layer(x, x_dtype, M, K, ldx, w_packed, s_w, group, bias, l1t, l1f, R, l2t, Re, y, ldy, N, ws, stream);
 }

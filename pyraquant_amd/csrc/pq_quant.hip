@@ -93,10 +93,11 @@ __device__ __forceinline__ float absmax_from_bits(uint32_t mag16) {
 template <int DT, int CH, bool PACKED>
 __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
-    int8_t* __restrict__ q, float* __restrict__ s, int64_t x_rows) {
+    int8_t* __restrict__ q, float* __restrict__ s, int64_t x_rows, int32_t* __restrict__ zero9) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int nvec = K >> 3;
+  if (zero9 && blockIdx.x == 0 && threadIdx.x < 9) zero9[threadIdx.x] = 0;
   if constexpr (PACKED) {
     if (m >= M) {
       if (m < ((M + 15) & ~15LL)) {
@@ -150,9 +151,10 @@ __global__ __launch_bounds__(256) void quant_rows_vec_kernel(
 template <int DT, bool PACKED>
 __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int K, int64_t M, const int32_t* __restrict__ row_idx,
-    int8_t* __restrict__ q, float* __restrict__ s, int64_t x_rows) {
+    int8_t* __restrict__ q, float* __restrict__ s, int64_t x_rows, int32_t* __restrict__ zero9) {
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (zero9 && blockIdx.x == 0 && threadIdx.x < 9) zero9[threadIdx.x] = 0;
   if constexpr (PACKED) {
     if (m >= M) {
       if (m < ((M + 15) & ~15LL)) {
@@ -188,7 +190,7 @@ __global__ __launch_bounds__(256) void quant_rows_scalar_kernel(
 
 template <int DT, bool PACKED>
 int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t x_rows, const int32_t* row_idx, int8_t* q,
-                 float* s, hipStream_t stream) {
+                 float* s, int32_t* zero9, hipStream_t stream) {
   const dim3 block(256);
   const int64_t rows = PACKED ? ((M + 15) & ~15LL) : M;
   if (const int st = check_grid((rows + 3) / 4, 256, "quant_rows")) return st;
@@ -200,7 +202,7 @@ int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t x_row
 #define PQ_QCASE(C)                                                                                       \
   if (need <= C) {                                                                                        \
     hipLaunchKernelGGL((quant_rows_vec_kernel<DT, C, PACKED>), grid, block, 0, stream, xp, ldx, (int)K, M, \
-                       row_idx, q, s, x_rows);                                                            \
+                       row_idx, q, s, x_rows, zero9);                                                     \
     return check_launch("quant_rows_vec");                                                                \
   }
     PQ_QCASE(1) PQ_QCASE(2) PQ_QCASE(3) PQ_QCASE(4) PQ_QCASE(5) PQ_QCASE(6) PQ_QCASE(8) PQ_QCASE(10)
@@ -208,7 +210,7 @@ int launch_quant(const void* x, int64_t M, int64_t K, int64_t ldx, int64_t x_row
 #undef PQ_QCASE
   }
   hipLaunchKernelGGL((quant_rows_scalar_kernel<DT, PACKED>), grid, block, 0, stream, xp, ldx, (int)K, M, row_idx,
-                     q, s, x_rows);
+                     q, s, x_rows, zero9);
   return check_launch("quant_rows_scalar");
 }
 
@@ -437,8 +439,10 @@ template <int DT, int NC, int W>   // W waves, NC: 64-wide K blocks per wave, K 
 __global__ __launch_bounds__(64 * W, 1) void quant_lowrank_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int64_t M, const int32_t* __restrict__ row_idx,
     const uint16_t* __restrict__ l1t, const uint16_t* __restrict__ l1f, int8_t* __restrict__ qp,
-    float* __restrict__ s, uint16_t* __restrict__ t, int64_t ldt, int nbatch) {
+    float* __restrict__ s, uint16_t* __restrict__ t, int64_t ldt, int nbatch, int32_t* __restrict__ zero9) {
   constexpr int K = 64 * W * NC, R = 32, NS = 2 * NC;
+  // (an older vector store than every DMA the ring counts: the vmcnt waits below only wait for it as well)
+  if (zero9 && blockIdx.x == 0 && threadIdx.x < 9) zero9[threadIdx.x] = 0;
   constexpr int CHUNKS = (2 * K + 1023) / 1024;      // 1 KB DMA pieces per row
   constexpr int PITCH = CHUNKS * 1024 + 64;          // LDS row pitch (+64 bytes: rows start 16 banks apart)
   __shared__ __attribute__((aligned(1024))) uint8_t xs[16 * PITCH];
@@ -650,8 +654,10 @@ template <int DT, int NCH, int RPW>   // NCH = K / 512: 16-byte chunks per lane 
 __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int64_t M, const int32_t* __restrict__ row_idx,
     const uint16_t* __restrict__ l1t, int8_t* __restrict__ qp, float* __restrict__ s, uint16_t* __restrict__ t,
-    int64_t ldt, int nbatch) {
+    int64_t ldt, int nbatch, int32_t* __restrict__ zero9) {
   constexpr int K = 512 * NCH;
+  // (an older vector store than every load the slab loop counts: the vmcnt waits below only wait for it as well)
+  if (zero9 && blockIdx.x == 0 && threadIdx.x < 9) zero9[threadIdx.x] = 0;
   constexpr int KW = kWideSlab / kWideWaves;   // 64: each wave's share of a slab, two MFMA K steps
   constexpr int BR = kWideWaves * RPW;         // rows per batch (16 or 8)
   static_assert(RPW == 1 || RPW == 2, "rows per wave");
@@ -883,13 +889,18 @@ extern "C" int pq_quant_rows(const void* x, int32_t x_dtype, int64_t M, int64_t 
   if (K > (1LL << 30) || M > (1LL << 40)) return set_error(PQ_ESHAPE, "pq_quant_rows: shape too large");
   if (x_rows < 1 || (!row_idx && x_rows < M))
     return set_error(PQ_ESHAPE, "pq_quant_rows: x_rows=%lld must cover the rows read", (long long)x_rows);
-  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, false>(x, M, K, ldx, x_rows, row_idx, q, s, stream);
-  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, false>(x, M, K, ldx, x_rows, row_idx, q, s, stream);
+  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, false>(x, M, K, ldx, x_rows, row_idx, q, s, nullptr, stream);
+  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, false>(x, M, K, ldx, x_rows, row_idx, q, s, nullptr, stream);
   return set_error(PQ_EDTYPE, "pq_quant_rows: unsupported dtype code %d", (int)x_dtype);
 }
 
 extern "C" int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
                                     const int32_t* row_idx, int8_t* qp, float* s, hipStream_t stream) {
+  return pq::quant_rows_packed_z(x, x_dtype, M, K, ldx, x_rows, row_idx, qp, s, nullptr, stream);
+}
+
+int pq::quant_rows_packed_z(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
+                            const int32_t* row_idx, int8_t* qp, float* s, int32_t* zero9, hipStream_t stream) {
   if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: bad shape M=%lld K=%lld", (long long)M, (long long)K);
   if (K % 64 != 0) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: K=%lld must be a multiple of 64", (long long)K);
   if (M == 0) return PQ_OK;
@@ -899,8 +910,8 @@ extern "C" int pq_quant_rows_packed(const void* x, int32_t x_dtype, int64_t M, i
   if (K > (1LL << 30) || M > (1LL << 40)) return set_error(PQ_ESHAPE, "pq_quant_rows_packed: shape too large");
   if (x_rows < 1 || (!row_idx && x_rows < M))
     return set_error(PQ_ESHAPE, "pq_quant_rows_packed: x_rows=%lld must cover the rows read", (long long)x_rows);
-  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, true>(x, M, K, ldx, x_rows, row_idx, qp, s, stream);
-  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, true>(x, M, K, ldx, x_rows, row_idx, qp, s, stream);
+  if (x_dtype == PQ_BF16) return launch_quant<PQ_BF16, true>(x, M, K, ldx, x_rows, row_idx, qp, s, zero9, stream);
+  if (x_dtype == PQ_F16) return launch_quant<PQ_F16, true>(x, M, K, ldx, x_rows, row_idx, qp, s, zero9, stream);
   return set_error(PQ_EDTYPE, "pq_quant_rows_packed: unsupported dtype code %d", (int)x_dtype);
 }
 
@@ -954,6 +965,12 @@ extern "C" int pq_lowrank_down(const void* x, int32_t dtype, int64_t M, int64_t 
 extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx,
                                      int64_t x_rows, const int32_t* row_idx, const void* l1t, const void* l1f,
                                      int64_t R, int8_t* qp, float* s, void* t, int64_t ldt, hipStream_t stream) {
+  return pq::quant_rows_lowrank_z(x, x_dtype, M, K, ldx, x_rows, row_idx, l1t, l1f, R, qp, s, t, ldt, nullptr, stream);
+}
+
+int pq::quant_rows_lowrank_z(const void* x, int32_t x_dtype, int64_t M, int64_t K, int64_t ldx, int64_t x_rows,
+                             const int32_t* row_idx, const void* l1t, const void* l1f, int64_t R, int8_t* qp, float* s,
+                             void* t, int64_t ldt, int32_t* zero9, hipStream_t stream) {
   if (M < 0 || K < 1) return set_error(PQ_ESHAPE, "pq_quant_rows_lowrank: bad shape M=%lld K=%lld", (long long)M, (long long)K);
   if (M == 0) return PQ_OK;
   if (!x || !qp || !s || !l1t || !t) return set_error(PQ_EINVAL, "pq_quant_rows_lowrank: null pointer");
@@ -980,7 +997,7 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
 #define PQ_QWCASE(D, NCH, RPW)                                                                                 \
     if (x_dtype == D && K == 512 * NCH) {                                                                      \
       hipLaunchKernelGGL((quant_lowrank_wide_kernel<D, NCH, RPW>), grid, dim3(64 * kWideWaves), 0, stream, xp,    \
-                         ldx, x_rows, M, row_idx, lp, qp, s, tp, ldt, nbatch);                                 \
+                         ldx, x_rows, M, row_idx, lp, qp, s, tp, ldt, nbatch, zero9);                          \
       return check_launch("quant_rows_lowrank");                                                               \
     }
     PQ_QWCASE(PQ_BF16, 8, 2) PQ_QWCASE(PQ_BF16, 12, 2) PQ_QWCASE(PQ_BF16, 16, 2) PQ_QWCASE(PQ_BF16, 20, 2)
@@ -990,7 +1007,7 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
 #undef PQ_QWCASE
   }
   if (!fused) {
-    const int st = pq_quant_rows_packed(x, x_dtype, M, K, ldx, x_rows, row_idx, qp, s, stream);
+    const int st = pq::quant_rows_packed_z(x, x_dtype, M, K, ldx, x_rows, row_idx, qp, s, zero9, stream);
     if (st != PQ_OK) return st;
     return pq_lowrank_down(x, x_dtype, M, K, ldx, x_rows, row_idx, l1t, R, t, ldt, stream);
   }
@@ -1004,7 +1021,7 @@ extern "C" int pq_quant_rows_lowrank(const void* x, int32_t x_dtype, int64_t M, 
 #define PQ_QLCASE(D, NC, W)                                                                                  \
   if (x_dtype == D && nc == NC) {                                                                           \
     hipLaunchKernelGGL((quant_lowrank_kernel<D, NC * 4 / W, W>), grid, dim3(64 * W), 0, stream, xp, ldx, x_rows, \
-                       M, row_idx, lp, fp, qp, s, tp, ldt, nbatch);                                         \
+                       M, row_idx, lp, fp, qp, s, tp, ldt, nbatch, zero9);                                  \
     return check_launch("quant_rows_lowrank");                                                              \
   }
   PQ_QLCASE(PQ_BF16, 4, 16) PQ_QLCASE(PQ_BF16, 5, 4) PQ_QLCASE(PQ_BF16, 8, 16) PQ_QLCASE(PQ_BF16, 10, 8)

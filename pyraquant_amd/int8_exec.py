@@ -123,6 +123,25 @@ def dequant_epilogue(acc: torch.Tensor, s_row: torch.Tensor, s_col: torch.Tensor
     return out
 
 
+# Scheduling buffers of the GEMM's persistent blocks (pq_int8_gemm's `sched`): 9 int32 counters per (device, stream),
+# zeroed once by torch and left zeroed by every launch, so the launches ordered on one stream share it. A stream
+# being captured into a graph gets none (the graph's launches take fixed shares), so a replay never shares a buffer
+# with eager launches on that stream.
+_SCHED: Dict[Tuple[int, int], torch.Tensor] = {}
+
+
+def _sched_buffer(dev: torch.device) -> Optional[torch.Tensor]:
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (idx, _raw_stream(dev))
+    buf = _SCHED.get(key)
+    if buf is None:
+        buf = torch.zeros(16, dtype=torch.int32, device=torch.device("cuda", idx))
+        _SCHED[key] = buf
+    return buf
+
+
 def _gemm(xq: torch.Tensor, s_row: torch.Tensor, w_int8: torch.Tensor, w_scale_k: torch.Tensor, group: int,
           bias: Optional[torch.Tensor], t: Optional[torch.Tensor], l2t: Optional[torch.Tensor],
           out_dtype: torch.dtype, out: Optional[torch.Tensor] = None,
@@ -158,7 +177,7 @@ def _gemm(xq: torch.Tensor, s_row: torch.Tensor, w_int8: torch.Tensor, w_scale_k
     _lib.check(L.pq_int8_gemm(_lib.ptr(xq), xq.stride(0), _lib.ptr(w_int8), w_int8.stride(0), _lib.ptr(s_row),
                               _lib.ptr(w_scale_k), group, _lib.ptr(bias), _lib.ptr(t), ldt, _lib.ptr(l2t), R, lr_code,
                               _lib.ptr(out), out.stride(0), _lib.dtype_code(out_dtype), _lib.ptr(ori), out.shape[0],
-                              M, N, K, _lib.stream_of(xq.device)), "int8_gemm")
+                              M, N, K, _lib.ptr(_sched_buffer(xq.device)), _lib.stream_of(xq.device)), "int8_gemm")
     return out
 
 
@@ -311,7 +330,8 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
     if out_dtype == torch.int32:
         c = torch.empty((M, N), dtype=torch.int32, device=xq_p.device)
         _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), None, None, 0, None, None, 0, None, 0, 0,
-                                         _lib.ptr(c), N, _lib.PQ_I32, None, 0, M, N, K, _lib.stream_of(xq_p.device)),
+                                         _lib.ptr(c), N, _lib.PQ_I32, None, 0, M, N, K, None,
+                                         _lib.stream_of(xq_p.device)),
                    "int8_gemm_packed")
         return c
     assert s_row.dtype == torch.float32 and s_row.is_contiguous() and s_row.numel() >= M
@@ -339,7 +359,8 @@ def int8_gemm_packed(xq_p: torch.Tensor, s_row: torch.Tensor, w_p: torch.Tensor,
     _lib.check(L.pq_int8_gemm_packed(_lib.ptr(xq_p), _lib.ptr(w_p), _lib.ptr(s_row), _lib.ptr(w_scale), group,
                                      _lib.ptr(bias), _lib.ptr(t), ldt, _lib.ptr(l2t), R, lr_code, _lib.ptr(out),
                                      out.stride(0), out_code, _lib.ptr(ori), out.shape[0], M, N, K,
-                                     _lib.stream_of(xq_p.device)), "int8_gemm_packed")
+                                     _lib.ptr(_sched_buffer(xq_p.device)), _lib.stream_of(xq_p.device)),
+               "int8_gemm_packed")
     return out
 
 
@@ -483,11 +504,13 @@ class Int8Linear(nn.Module):
     def _lr_frag(self) -> Optional[torch.Tensor]:
         """lr_At in fragment order, repacked whenever lr_At is not the tensor it was packed from: a module-wide cast
         or move, load_state_dict (which copies into lr_At in place) or any other in-place update (torch's version
-        counter). None where no fragment order exists for lr_At's shape."""
+        counter). Tensors made under torch.inference_mode() carry no version counter: for them the key is the
+        storage, dtype and device alone, so an in-place edit of an inference-mode lr_At needs the module rebuilt.
+        None where no fragment order exists for lr_At's shape."""
         At = self.lr_At
         if At is None:
             return None
-        key = (At.data_ptr(), At._version, At.dtype, At.device)
+        key = (At.data_ptr(), None if At.is_inference() else At._version, At.dtype, At.device)
         if key != self._lr_frag_key:
             self.lr_At_frag = pack_lowrank_l1t(At) if At.is_cuda and At.is_contiguous() else None
             self._lr_frag_key = key

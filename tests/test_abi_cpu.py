@@ -66,13 +66,13 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     # GEMM: K % 64, N % 64, alignment, group, rank
     p16 = ctypes.c_void_p(256)
     args = dict(a=p16, lda=128, w=p16, ldw=128, s_row=p16, s_w=p16, group=0, bias=nul, t=nul, ldt=0, l2t=nul, R=0,
-                lr=0, c=p16, ldc=128, od=0, ori=nul, c_rows=0, M=8, N=128, K=128, st=nul)
+                lr=0, c=p16, ldc=128, od=0, ori=nul, c_rows=0, M=8, N=128, K=128, sched=nul, st=nul)
 
     def gemm(**kw):
         a = dict(args, **kw)
         return lib.pq_int8_gemm(a["a"], a["lda"], a["w"], a["ldw"], a["s_row"], a["s_w"], a["group"], a["bias"],
                                 a["t"], a["ldt"], a["l2t"], a["R"], a["lr"], a["c"], a["ldc"], a["od"], a["ori"],
-                                a["c_rows"], a["M"], a["N"], a["K"], a["st"])
+                                a["c_rows"], a["M"], a["N"], a["K"], a["sched"], a["st"])
 
     assert gemm(K=96, lda=96, ldw=96) == L.PQ_ESHAPE
     assert gemm(N=96) == L.PQ_ESHAPE
@@ -85,12 +85,17 @@ def test_invalid_arguments_rejected_without_gpu(lib):
     assert gemm(t=p16, l2t=nul, R=32, ldt=32) == L.PQ_EINVAL
     assert gemm(t=p16, l2t=p16, R=32, ldt=(1 << 22) + 8) == L.PQ_ESHAPE   # t rows at 32-bit buffer offsets
     assert lib.pq_int8_gemm_packed(p16, p16, p16, p16, 0, nul, p16, (1 << 22) + 8, p16, 32, 0, p16, 128, 0, nul, 0,
-                                   8, 128, 128, nul) == L.PQ_ESHAPE
+                                   8, 128, 128, nul, nul) == L.PQ_ESHAPE
+    # the scheduling buffer holds int32 counters
+    assert gemm(sched=ctypes.c_void_p(258)) == L.PQ_EALIGN
+    assert lib.pq_int8_gemm_packed(p16, p16, p16, p16, 0, nul, nul, 0, nul, 0, 0, p16, 128, 0, nul, 0,
+                                   8, 128, 128, ctypes.c_void_p(258), nul) == L.PQ_EALIGN
+    assert b"sched" in lib.pq_last_error()
     # a scatter needs the canvas's row count
     assert gemm(ori=p16, c_rows=0) == L.PQ_ESHAPE
     assert b"c_rows" in lib.pq_last_error()
     assert lib.pq_int8_gemm_packed(p16, p16, p16, p16, 0, nul, nul, 0, nul, 0, 0, p16, 128, 0, p16, 0,
-                                   8, 128, 128, nul) == L.PQ_ESHAPE
+                                   8, 128, 128, nul, nul) == L.PQ_ESHAPE
     assert gemm(od=5) == L.PQ_EDTYPE or gemm(od=5) == L.PQ_ELAUNCH
     assert gemm(M=0) == L.PQ_OK
     assert lib.pq_int8_gemm_i32(p16, 128, p16, 128, nul, 128, 8, 128, 128, nul) == L.PQ_EINVAL

@@ -1,17 +1,23 @@
-"""Full-size parity: Int8Linear.forward at every benchmark configuration's real shape (c1, c2a, c2b, c3, c4), checked
-against the CPU oracle on sampled rows (deploy/int8_exec.py:382-393 for the layer, :303-309 for the epilogue order).
+"""Full-size parity: Int8Linear.forward at every benchmark configuration's real shape (c0, c1, c2a, c2b, c3 in bf16 as
+the configuration states it and in fp16, c4), checked against the CPU oracle on sampled rows (deploy/int8_exec.py:382-393
+for the layer, :303-309 for the epilogue order).
 
-Each case runs the whole layer on the GPU (the module's own path: the fused quantizer + low-rank pass or the packed
-quantizer, then the packed GEMM with its epilogue), then takes 64 seeded random rows plus the last 40 rows (the last,
-possibly ragged, tiles) and computes those rows on the CPU with the oracle from the module's own int8 weights:
-* int8 codes and row scales bit-exact (the codes are read back from the packed buffer the layer's first kernel
-  wrote, through the same entry point the module calls);
+Each unrouted case runs the whole layer on the GPU twice: through the module (Int8Linear.forward, whose common call is
+one pq_int8_linear per layer), and through pq_int8_linear directly with a workspace the test holds. The two outputs
+must be bit-identical, and the int8 codes and row scales are read back from that workspace: the packed buffer and
+the scales the layer's first kernel staged for its GEMM. The test then takes 64 seeded random rows plus the last 40
+rows (the last, possibly ragged, tiles) and computes those rows on the CPU with the oracle from the module's own int8
+weights:
+* int8 codes and row scales bit-exact;
 * without a low-rank branch (c3), the 16-bit outputs bit-exact;
 * with one, the normwise bar (max 1e-2, mean 5e-3) and the element-wise bar of conftest.elem_violation.
-The routed case (c4) runs on the full 65536-row canvas: the routed rows land where the gather list says, every other
-row of the canvas is left as it was. A last case runs c1 at batch 2 (131584 rows), whose output rows lie past 2 GiB
-of byte offset.
+The routed case (c4) runs on the full 65536-row canvas through the general path (the gathering quantizer, then the
+scattering GEMM): the routed rows land where the gather list says, every other row of the canvas is left as it was;
+its codes come from a second call of the gathering quantizer. A last case runs c1 at batch 2 (131584 rows), whose
+output rows lie past 2 GiB of byte offset.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -43,11 +49,35 @@ def _packed_rows(qp: torch.Tensor, rows: torch.Tensor, K: int) -> np.ndarray:
 
 
 def _first_stage(E, q, x2, row_idx=None):
-    """The codes, scales (and t) of the layer's first kernel, through the entry point Int8Linear.forward uses."""
+    """The codes, scales (and t) of the routed layer's first kernel, through the entry point its general path uses."""
     if q.lr_At is not None:
         return E.quant_rows_lowrank(x2, q.lr_At, row_idx, q._lr_frag())
     xq, sx = E.quant_rows_packed(x2, row_idx)
     return xq, sx, None
+
+
+def _layer_call(q, x):
+    """The layer through pq_int8_linear with a workspace held here (filled with 0xA5 first, so nothing is read from a
+    clean buffer): (y, packed codes, row scales) with the codes and scales read from that workspace. Its layout for M
+    rows and K inputs: the packed codes at byte 0 (ceil(M / 16) * 16 * K bytes), the fp32 row scales from the next
+    256-byte boundary."""
+    from pyraquant_amd import _lib
+
+    L = _lib.load()
+    M, K = x.shape
+    N = q.out_features
+    R = 0 if q.lr_At is None else q.lr_At.shape[0]
+    Re = 0 if q.lr_Bt is None else q.lr_Bt.shape[1]
+    ws = torch.full((L.pq_int8_linear_workspace_size(M, K, R),), 0xA5, dtype=torch.uint8, device=x.device)
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
+    frag = q._lr_frag() if R else None
+    _lib.check(L.pq_int8_linear(p(x), _lib.dtype_code(x.dtype), M, K, x.stride(0), p(q.weight_packed), p(q._scale_k()),
+                                q.group_size, p(q.bias), p(q.lr_At), p(frag), R, p(q.lr_Bt), Re, p(y), N, N, p(ws),
+                                ws.numel(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "pq_int8_linear")
+    qb = (M + 15) // 16 * 16 * K
+    so = (qb + 255) // 256 * 256
+    return y, ws[:qb].view(torch.int8), ws[so:so + 4 * M].view(torch.float32)
 
 
 def _check_rows(oracle, q, x_rows_bits, dt, y_rows, codes, scales):
@@ -69,18 +99,20 @@ def _check_rows(oracle, q, x_rows_bits, dt, y_rows, codes, scales):
     assert v <= 1.0, v
 
 
-@pytest.mark.parametrize("cfg", ["c1", "c2a", "c2b", "c3_1280", "c3_5120"])
+@pytest.mark.parametrize("cfg", ["c0", "c1", "c2a", "c2b", "c3_1280", "c3_5120", "c3_1280_f16", "c3_5120_f16"])
 def test_layer_full_size(oracle, cuda, cfg):
     from pyraquant_amd import int8_exec as E
     from pyraquant_amd.workloads import CONFIGS, make_linear, make_x
 
     c = CONFIGS[cfg]
-    print(f"[fullsize] {cfg} M={c.M} K={c.K} N={c.N} rank={c.lowrank} group={c.group}", flush=True)
+    print(f"[fullsize] {cfg} M={c.M} K={c.K} N={c.N} rank={c.lowrank} group={c.group} dtype={c.dtype}", flush=True)
     q = E.Int8Linear(make_linear(c.K, c.N, c.lowrank, c.bias, dtype=c.dtype), device=cuda, group_size=c.group)
     x = make_x(c.M, c.K, c.dtype, seed=7, device=cuda)
     y = q(x)
     assert y.shape == (c.M, c.N) and y.dtype == c.dtype
-    xq, sx, _ = _first_stage(E, q, x)
+    y2, xq, sx = _layer_call(q, x)
+    assert torch.equal(y2, y), "pq_int8_linear and Int8Linear.forward differ"
+    del y2
     rows = _sample_rows(c.M, seed=c.M + c.N)
     rd = rows.to(cuda)
     _check_rows(oracle, q, bits(x[rd]), dcode(c.dtype), y[rd], _packed_rows(xq, rows, c.K), sx[rd].cpu().numpy())
@@ -128,6 +160,8 @@ def test_layer_output_beyond_2gib(oracle, cuda):
     g = torch.Generator().manual_seed(12)
     rows = torch.cat([first + torch.randperm(M - 40 - first, generator=g)[:24], torch.arange(M - 40, M)])
     rows = rows.sort().values
-    xq, sx, _ = _first_stage(E, q, x)
+    y2, xq, sx = _layer_call(q, x)
+    assert torch.equal(y2, y), "pq_int8_linear and Int8Linear.forward differ"
+    del y2
     rd = rows.to(cuda)
     _check_rows(oracle, q, bits(x[rd]), dcode(c.dtype), y[rd], _packed_rows(xq, rows, c.K), sx[rd].cpu().numpy())

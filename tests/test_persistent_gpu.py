@@ -1,11 +1,14 @@
-"""The persistent 256 x 256 GEMM (one workgroup per CU looping over tiles). With a per-stream scheduling buffer the
-workgroups claim tiles from per-XCD counters and the last one out zeroes them again; under graph capture and in
-the allocation-free layer call the tiles follow a fixed per-workgroup share instead. Every schedule must produce
-every tile exactly as the one-tile-per-workgroup kernels do:
+"""The persistent 256 x 256 GEMM (one workgroup per CU looping over tiles). With a scheduling buffer (the caller's:
+the GEMM entries' `sched`, which the Python layer keeps per stream, or the slice of pq_int8_linear's workspace that
+its quantizer kernel zeroes) the workgroups claim tiles from per-XCD counters and the last one out zeroes them
+again; without one (a stream under graph capture in the Python layer) the tiles follow a fixed per-workgroup share.
+Every schedule must produce every tile exactly as the one-tile-per-workgroup kernels do:
 * consecutive launches on one stream, each into a NaN-filled output (a counter left non-zero by a launch would make
   the next one skip tiles);
 * two streams running large GEMMs at the same time (each stream has its own buffer);
 * a captured graph replayed between eager launches (the graph keeps the fixed share);
+* the single-call layer with a freshly allocated workspace whose bytes hold garbage, eagerly and replayed from a
+  graph (its quantizer kernel zeroes the counters each time);
 * the allocation-free layer call against the workspace call at a size that runs persistent blocks.
 The reference is the same product computed in 256-row slices, whose few blocks run one tile per workgroup with the
 same per-element epilogue arithmetic, so the results agree bit for bit."""
@@ -148,3 +151,58 @@ def test_noalloc_layer_at_a_persistent_size(cuda):
         assert torch.equal(y_na, y_ws), f"call {i}"
         y_ws.fill_(float("nan"))
         y_na.fill_(float("nan"))
+
+
+def test_layer_call_fresh_workspace_and_graph(cuda):
+    """pq_int8_linear on a workspace fresh from torch.empty, filled with garbage first (a scheduling buffer left as
+    found would start the claims past the end and leave tiles unwritten): eager calls into NaN-filled outputs, then a
+    captured call replayed three times with an eager call on another workspace between the replays. Every output
+    equals the layer computed in 256-row slices."""
+    from pyraquant_amd import _lib
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    L = _lib.load()
+    Mx, Kx, Nx = 4096, 3072, 8192            # 16 x 32 = 512 blocks of 256 x 256: persistent
+    q = E.Int8Linear(make_linear(Kx, Nx, 32, True, seed=15, dtype=torch.bfloat16), device=cuda)
+    x = make_x(Mx, Kx, torch.bfloat16, seed=16, device=cuda)
+    ref = torch.cat([q(x[r0:r0 + 256]) for r0 in range(0, Mx, 256)])
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())
+    size = L.pq_int8_linear_workspace_size(Mx, Kx, 32)
+
+    def call(ws, y):
+        args = [p(x), _lib.dtype_code(x.dtype), Mx, Kx, x.stride(0), p(q.weight_packed), p(q._scale_k()), 0, p(q.bias),
+                p(q.lr_At), p(q._lr_frag()), 32, p(q.lr_Bt), q.lr_Bt.shape[1], p(y), Nx, Nx, p(ws), ws.numel(),
+                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)]
+        _lib.check(L.pq_int8_linear(*args), "pq_int8_linear")
+
+    for i, fill in enumerate((0xFF, 0x5A, 0x01)):
+        ws = torch.empty(size, dtype=torch.uint8, device=cuda)
+        ws.fill_(fill)
+        y = torch.full((Mx, Nx), float("nan"), dtype=x.dtype, device=cuda)
+        call(ws, y)
+        torch.cuda.synchronize()
+        print(f"[persistent] layer call, fresh workspace filled with {fill:#x}", flush=True)
+        assert torch.equal(y, ref), f"eager call {i}"
+    ws_g = torch.full((size,), 0x77, dtype=torch.uint8, device=cuda)
+    ws_e = torch.empty(size, dtype=torch.uint8, device=cuda)
+    y_g = torch.empty((Mx, Nx), dtype=x.dtype, device=cuda)
+    y_e = torch.empty_like(y_g)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        call(ws_g, y_g)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(ws_g, y_g)
+    for i in range(3):
+        y_g.fill_(float("nan"))
+        y_e.fill_(float("nan"))
+        ws_e.fill_(0xC3)
+        g.replay()
+        call(ws_e, y_e)
+        torch.cuda.synchronize()
+        print(f"[persistent] layer call, graph replay {i}", flush=True)
+        assert torch.equal(y_g, ref), f"replay {i}"
+        assert torch.equal(y_e, ref), f"eager call beside replay {i}"
