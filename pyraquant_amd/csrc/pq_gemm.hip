@@ -20,9 +20,11 @@
 // LDS-DMA buffer loads (buffer_load_dwordx4 ... lds): no VGPR staging, no ds_write, and NS - 1 stages of
 // prefetch in flight to cover L2 / MALL latency. One DMA instruction fills 1 KB = 16 LDS rows of 64 bytes;
 // each lane fetches the 16-byte chunk that the XOR swizzle places at its LDS slot, so the MFMA operand reads
-// (ds_read_b128, one tile row per lane) are bank-conflict free. The two 32-byte K substeps of a stage are
-// software-pipelined: the fragments of the next substep are read from LDS while the MFMAs of the current one
-// run, and the DMA of a new stage is interleaved with the MFMAs. One workgroup barrier per stage.
+// (ds_read_b128, one tile row per lane) are bank-conflict free. In the 8-wave 256 x 256 blocks the two wave groups
+// ping-pong: per SIMD, one wave issues a stage's MFMAs back to back while the other reads the next stage's fragments
+// and issues its DMA, swapping at each of two workgroup barriers per stage. In the 4-wave blocks the two 32-byte K
+// substeps of a stage are software-pipelined instead: the fragments of the next substep are read from LDS while the
+// MFMAs of the current one run, and the DMA of a new stage is interleaved with the MFMAs; one barrier per stage.
 //
 // Group-32 runs on the same kernel (MODE kModeGroup32): every 32-wide K substep is one K group, whose int32 partial
 // (one MFMA from zero) the VALU converts and fma's with s_w[g, n] into an fp32 accumulator held in VGPRs, groups in
@@ -525,6 +527,8 @@ void gemm_dma_kernel(const GemmArgs p) {
   // XCDs' lists. The XCDs of one chip run the loop at different speeds (up to 5 % apart), so fixed shares finish
   // up to 165 us apart at c1. Without the buffer it steps vb by the grid size (a fixed share per workgroup).
   constexpr bool PERSIST = persistent_block<TI, TJ, WMW, NS, OCC, MODE, LRS, LRDT, ODT, ACC>();
+  // Ping-pong main loop for the 8-wave 256 x 256 blocks (see below); the 4-wave blocks interleave instead.
+  constexpr bool PP = NW == 8 && OCC == 1 && !G32;
   const int nbt = p.tiles_m * p.tiles_n;
   // Claims (lane 0 of wave 0). XCD x's list holds cnt(x) tiles, of which first(x) went out as first tiles.
   const int x0 = blockIdx.x & 7;
@@ -788,47 +792,95 @@ void gemm_dma_kernel(const GemmArgs p) {
   // Prologue: all NS stages go out at once; the first barrier waits for stage 0 only (the explicit barrier: a
   // fenced one would wait for every DMA in flight). Issuing stages 1 .. NS - 1 only after stage 0 had landed put a
   // second memory latency in front of every tile.
-#pragma unroll
-  for (int st = 0; st < NS; ++st) {
-    if (st < KT) dma(st, st);
-    else dma_tail(st, st);
-  }
-  wait_dma<(NS - 1) * DPW>();   // this wave's stage 0 has landed
-  lds_barrier();                // every wave's has
-  __builtin_amdgcn_sched_barrier(0);
-  rd(f0, 0, 0);
-  auto iter = [&](int kt, int b, int bn, auto tail) {
-    rd(f1, b, 1);
-    mm(f0, kt, 0);
-    interleave(no_dma{});
-    wait_dma<(NS - 2) * DPW>();   // this wave's DMA of stage kt + 1 has landed
-    lds_barrier();                // every wave's has, and every wave is done reading buffer b
-    __builtin_amdgcn_sched_barrier(0);
-    rd(f0, bn, 0);
-    if constexpr (decltype(tail)::value) dma_tail(b, kt + NS);
-    else dma(b, kt + NS);
-    mm(f1, kt, 1);
-    interleave(with_dma{});
-  };
-  int b = 0;
-  int kt = 0;
-  for (; kt < KT - NS; ++kt) {      // stages kt + NS < KT: operand DMA
-    const int bn = b + 1 == NS ? 0 : b + 1;
-    iter(kt, b, bn, no_dma{});
-    b = bn;
-  }
-  for (; kt < KT - 1; ++kt) {       // the last NS - 1 iterations: epilogue operands (dma_tail)
-    const int bn = b + 1 == NS ? 0 : b + 1;
-    iter(kt, b, bn, with_dma{});
-    b = bn;
-  }
-  // last stage: the epilogue's operands are fetched under its MFMAs
   Epi epi;
   const int nbase = n0 + wn * (BN / 2), mbase = m0 + wm * (BM / WMW);
-  if constexpr (!ELDS) epi.prefetch_rows(p, mbase, lane);
-  rd(f1, b, 1);
-  mm(f0, KT - 1, 0);
-  mm(f1, KT - 1, 1);
+  if constexpr (PP) {
+    // Ping-pong. Waves 0-3 (group A) and 4-7 (group B) hold one wave per SIMD each. Time is cut into slots ended
+    // by workgroup barriers; in every slot one group runs a compute phase (a stage's 16 MFMAs back to back, from
+    // fragments already in registers) while the other runs a memory phase (the next stage's 12 fragment reads and
+    // its share of a DMA), group B one slot behind group A:
+    //   slot 2s: A reads stage s, B computes stage s - 1;   slot 2s + 1: A computes stage s, B reads stage s.
+    // So each SIMD's MFMA pipe is fed by one wave at a time in runs of 16. Two waves that both interleave MFMAs and
+    // LDS reads alternate issue instruction by instruction, which costs pipe cycles (c1 GEMM: 70 % -> 73 % MFMA busy,
+    // 3-4 % faster; c2a, c2b 2.5 % faster; outputs bit-identical).
+    // The ring: the prologue issues stages 0 .. NS - 2; the memory phase of stage s issues stage s + NS - 1 into the
+    // buffer of stage s - 1, which both groups have read by then. Stage s + 1 must have landed (every wave's DMA)
+    // at the barrier that ends slot 2s + 1: group A waits at the end of its compute phase, group B at the end of its
+    // memory phase, each for all but its NS - 2 younger stages (vmcnt((NS - 2) DPW)), as in the interleaved loop.
+    // Each group passes 2 KT + 2 barriers: B idles in the first slot, A in the last.
+    const bool grp_b = wave >= NW / 2;
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) {
+      if (st < KT) dma(st, st);
+      else dma_tail(st, st);
+    }
+    wait_dma<(NS - 2) * DPW>();   // this wave's stage 0 has landed
+    lds_barrier();                // every wave's has
+    if (grp_b) lds_barrier();     // group B: one idle slot
+    int b = 0;
+    auto slot_pair = [&](int s, auto tail) {
+      // memory phase: both substeps' fragments of stage s, and this wave's DMA of stage s + NS - 1 into the buffer of
+      // stage s - 1, which every wave has read (group A read it two slots ago, group B one slot ago)
+      rd(f0, b, 0);
+      rd(f1, b, 1);
+      const int bd = b == 0 ? NS - 1 : b - 1;
+      if constexpr (decltype(tail)::value) dma_tail(bd, s + NS - 1);
+      else dma(bd, s + NS - 1);
+      if (grp_b) wait_dma<(NS - 2) * DPW>();   // stage s + 1 has landed (group B: at the end of its memory phase)
+      lds_barrier();
+      // compute phase: 16 MFMAs back to back
+      mm(f0, s, 0);
+      mm(f1, s, 1);
+      if (!grp_b) wait_dma<(NS - 2) * DPW>();  // group A: at the end of its compute phase
+      lds_barrier();
+      b = b + 1 == NS ? 0 : b + 1;
+    };
+    int s = 0;
+    for (; s < KT - NS + 1; ++s) slot_pair(s, std::integral_constant<bool, false>{});
+    for (; s < KT; ++s) slot_pair(s, std::integral_constant<bool, true>{});
+    if (!grp_b) lds_barrier();    // group A: one idle slot while group B computes the last stage
+    if constexpr (!ELDS) epi.prefetch_rows(p, mbase, lane);
+  } else {
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      if (st < KT) dma(st, st);
+      else dma_tail(st, st);
+    }
+    wait_dma<(NS - 1) * DPW>();   // this wave's stage 0 has landed
+    lds_barrier();                // every wave's has
+    __builtin_amdgcn_sched_barrier(0);
+    rd(f0, 0, 0);
+    auto iter = [&](int kt, int b, int bn, auto tail) {
+      rd(f1, b, 1);
+      mm(f0, kt, 0);
+      interleave(no_dma{});
+      wait_dma<(NS - 2) * DPW>();   // this wave's DMA of stage kt + 1 has landed
+      lds_barrier();                // every wave's has, and every wave is done reading buffer b
+      __builtin_amdgcn_sched_barrier(0);
+      rd(f0, bn, 0);
+      if constexpr (decltype(tail)::value) dma_tail(b, kt + NS);
+      else dma(b, kt + NS);
+      mm(f1, kt, 1);
+      interleave(with_dma{});
+    };
+    int b = 0;
+    int kt = 0;
+    for (; kt < KT - NS; ++kt) {      // stages kt + NS < KT: operand DMA
+      const int bn = b + 1 == NS ? 0 : b + 1;
+      iter(kt, b, bn, no_dma{});
+      b = bn;
+    }
+    for (; kt < KT - 1; ++kt) {       // the last NS - 1 iterations: epilogue operands (dma_tail)
+      const int bn = b + 1 == NS ? 0 : b + 1;
+      iter(kt, b, bn, with_dma{});
+      b = bn;
+    }
+    // last stage: the epilogue's operands are fetched under its MFMAs
+    if constexpr (!ELDS) epi.prefetch_rows(p, mbase, lane);
+    rd(f1, b, 1);
+    mm(f0, KT - 1, 0);
+    mm(f1, KT - 1, 1);
+  }
   wait_dma<0>();     // the epilogue operands, and the out-of-range DMAs of the last iterations, have landed
   __syncthreads();   // every wave is done reading the ring: it becomes the output staging area
   // the own-list claim of the next tile goes out now; its result is read after the epilogue, which covers its latency

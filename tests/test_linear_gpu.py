@@ -440,3 +440,26 @@ def test_int8linear_module_cast(oracle, cuda):
         else:
             mx, mean = rel_errors(oracle.to_f32(bits(yh), 1), o["y"])
             assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
+def test_int8linear_under_inference_mode(cuda):
+    """Int8Linear built and run inside torch.inference_mode(): inference tensors carry no version counter, so the
+    fragment-order copy of lr_At is keyed on its storage, dtype and device there. A rank-32 layer (whose quantizer
+    reads that copy) built and called under inference_mode gives the bits of the same layer built outside it, and
+    so does a module conversion under inference_mode."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    lin = make_linear(3072, 1024, 32, True, seed=21)
+    x = make_x(300, 3072, seed=22).to(cuda)
+    ref = E.Int8Linear(lin, device=cuda)(x)
+    with torch.inference_mode():
+        q = E.Int8Linear(lin, device=cuda)
+        assert q.lr_At.is_inference() and q.lr_At_frag is not None
+        y = q(x)
+        assert torch.equal(q(x), y)                  # the cached fragment copy is reused
+        model = torch.nn.Sequential(make_linear(3072, 1024, 32, True, seed=21)).to(cuda)
+        E.convert_linears_to_int8(model, device=cuda)
+        y2 = model(x)
+    assert torch.equal(y, ref)
+    assert torch.equal(y2, ref)
