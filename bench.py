@@ -37,8 +37,8 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=16384, help="row sample of the CPU baseline")
     ap.add_argument("--cpu-iters", type=int, default=5)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
-                    help="only run 3 device-to-device copies of BYTES (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE "
-                         "against a plain copy kernel of known size) and exit")
+                    help="only run device-to-device copies of BYTES (3 to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE "
+                         "against a plain copy kernel of known size, then 10 timed: its read + write rate) and exit")
     ap.add_argument("--no-side", action="store_true",
                     help="skip the side measurements (routing kernels, SDXL small-M launches, weight fold), e.g. for "
                          "profiler runs that should hold the layer's kernels only")
@@ -65,12 +65,24 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     if args.copy_probe:
+        # 3 device-to-device copies of BYTES (the PMC calibration), then 10 more timed by HIP events: the read + write
+        # rate of a plain copy kernel, the practical roofline of a pass that reads and writes HBM at once
         src = torch.ones(args.copy_probe // 4, dtype=torch.int32, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": src.numel() * 4}), flush=True)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / 10 * 1e3
+        nb = src.numel() * 4
+        print(json.dumps({"copy_probe_bytes": nb, "copy_us": round(us, 1),
+                          "read_plus_write_GBps": round(2 * nb / us / 1e3, 1),
+                          "frac_hbm": round(2 * nb / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
         return 0
     cfg = CONFIGS[args.config]
     if args.blaslt:

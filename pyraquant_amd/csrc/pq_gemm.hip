@@ -509,8 +509,11 @@ void gemm_dma_kernel(const GemmArgs p) {
   constexpr int kRest = TI * TJ - NF;         // MFMAs of a substep beyond the NF that carry a fragment read
   constexpr int kVPer = kRest > 0 ? (DPW + kRest - 1) / (kRest > 0 ? kRest : 1) : 0;   // DMA per such MFMA
   static_assert(NS >= 3 && (NS * STAGE + SLOTS * SB) * OCC <= 160 * 1024, "LDS ring");
+  // LDS: the group-32 scale slots first, then the operand ring. With the scales at the start their LDS reads fit the
+  // 16-bit immediate offset of ds_read (past a 64 KB ring they cost a v_add each); SLOTS * SB is a multiple of 1 KB.
   __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE + SLOTS * SB];
-  uint8_t* const sscale = smem + NS * STAGE;
+  uint8_t* const sscale = smem;
+  uint8_t* const ring = smem + SLOTS * SB;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -611,7 +614,7 @@ void gemm_dma_kernel(const GemmArgs p) {
   }
 
   auto dma = [&](int buf, int kt) {
-    uint8_t* sb = smem + buf * STAGE;
+    uint8_t* sb = ring + buf * STAGE;
     const int koff = kt < KT ? (rev ? KT - 1 - kt : kt) * kStageStep : kOOB;
 #pragma unroll
     for (int i = 0; i < DW; ++i)
@@ -641,7 +644,7 @@ void gemm_dma_kernel(const GemmArgs p) {
   auto dma_tail = [&](int buf, int st) {
     if constexpr (ELDS) {
       if (st == KT || st == KT + 1) {
-        uint8_t* sb = smem + buf * STAGE;
+        uint8_t* sb = ring + buf * STAGE;
         const bool rows = st == KT;
         const int nsl = rows ? kRowSlots : kColSlots;
         const int rows_x = rows ? rows_a : rows_w;
@@ -707,7 +710,7 @@ void gemm_dma_kernel(const GemmArgs p) {
 
   v4i f0[NF], f1[NF];
   auto rd = [&](v4i (&f)[NF], int buf, int s) {
-    const uint8_t* sb = smem + buf * STAGE;
+    const uint8_t* sb = ring + buf * STAGE;
     const int c = ((2 * s + kh) ^ sw) << 4;
 #pragma unroll
     for (int i = 0; i < TI; ++i) f[i] = *reinterpret_cast<const v4i*>(sb + fw_off + i * 32 * kBKd + c);
@@ -890,19 +893,19 @@ void gemm_dma_kernel(const GemmArgs p) {
     // buffers of stages KT (rows) and KT + 1 (columns) hold the operands; staging in the NS - 2 others
     constexpr int kSpb = STAGE / Epi::kStageBytesL;
     const int k = wave / kSpb;
-    uint8_t* stage = smem + ((KT + 2 + k) % NS) * STAGE + (wave % kSpb) * Epi::kStageBytesL;
-    epi.run_lds(p, acc, wn * (BN / 2), wm * (BM / WMW), nbase, mbase, lane, stage, smem + ((KT + 1) % NS) * STAGE,
-                smem + (KT % NS) * STAGE);
+    uint8_t* stage = ring + ((KT + 2 + k) % NS) * STAGE + (wave % kSpb) * Epi::kStageBytesL;
+    epi.run_lds(p, acc, wn * (BN / 2), wm * (BM / WMW), nbase, mbase, lane, stage, ring + ((KT + 1) % NS) * STAGE,
+                ring + (KT % NS) * STAGE);
   } else {
     static_assert(ELDS || NW * Epi::kStageBytes <= NS * STAGE, "output staging must fit the LDS ring");
-    epi.run(p, acc, nbase, mbase, lane, smem + wave * Epi::kStageBytes);
+    epi.run(p, acc, nbase, mbase, lane, ring + wave * Epi::kStageBytes);
   }
   if constexpr (PERSIST) {
     // The next tile reaches every wave through the last 4 bytes of the row-operand buffer: its last DMA slot is
     // past the row operands (kRowSlots < 32), so the epilogue never reads it, and the next tile's DMA overwrites it
     // only after the second barrier.
     static_assert(kRowSlots < NW * (DW + DA), "the row buffer's last slot holds no epilogue operand");
-    int* const slot = reinterpret_cast<int*>(smem + (KT % NS) * STAGE + STAGE - 4);
+    int* const slot = reinterpret_cast<int*>(ring + (KT % NS) * STAGE + STAGE - 4);
     if (wave == 0 && lane == 0) *slot = claim_rest(vb, own);
     lds_barrier();
     vb = *slot;
