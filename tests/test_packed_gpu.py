@@ -151,10 +151,12 @@ def test_int8linear_packed_path(oracle, cuda, cfg, M):
     assert torch.equal(y, ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(8191, 6464, 1280), (16400, 4160, 192), (16400, 4160, 64)])
+@pytest.mark.parametrize("M,N,K", [(8191, 6464, 1280), (16400, 4160, 192), (16400, 4160, 64), (16400, 4160, 256),
+                                   (16400, 4160, 320)])
 def test_gemm_big_tile_path_ragged(oracle, cuda, M, N, K):
-    """Shapes with >= 1024 tiles of 256 x 128 take the 256 x 256 block of 8 waves; ragged M and N (tail tiles on
-    both edges) stay exact there, row-major and packed, and the fused outputs agree bit for bit."""
+    """Shapes with >= 1024 tiles of 256 x 128 take the 256 x 256 block of 8 waves (the ping-pong main loop, whose
+    prologue issues 4 stages: K = 64 - 320 put the end of K inside, at and just past it); ragged M and N (tail tiles
+    on both edges) stay exact there, row-major and packed, and the fused outputs agree bit for bit."""
     from pyraquant_amd import int8_exec as E
 
     a, w = _codes(M, N, K, M + N, cuda)
