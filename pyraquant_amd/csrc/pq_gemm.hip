@@ -789,12 +789,13 @@ void gemm_dma_kernel(const GemmArgs p) {
   using no_dma = std::integral_constant<bool, false>;
   using with_dma = std::integral_constant<bool, true>;
 
-  // Ring: stage s lives in buffer s % NS. The DMA of stage s is issued after the barrier of iteration s - NS and
-  // must have landed at the barrier that ends iteration s - 1, NS - 1 iterations later; in between, the DMAs of
-  // NS - 2 younger stages may still be in flight, hence vmcnt((NS - 2) * DPW).
-  // Prologue: all NS stages go out at once; the first barrier waits for stage 0 only (the explicit barrier: a
-  // fenced one would wait for every DMA in flight). Issuing stages 1 .. NS - 1 only after stage 0 had landed put a
-  // second memory latency in front of every tile.
+  // Ring: stage s lives in buffer s % NS. In the interleaved loop (the else branch below) the DMA of stage s is
+  // issued after the barrier of iteration s - NS and must have landed at the barrier that ends iteration s - 1,
+  // NS - 1 iterations later; in between, the DMAs of NS - 2 younger stages may still be in flight, hence
+  // vmcnt((NS - 2) * DPW). Its prologue issues all NS stages at once; the first barrier waits for stage 0 only (the
+  // explicit barrier: a fenced one would wait for every DMA in flight). Issuing stages 1 .. NS - 1 only after stage 0
+  // had landed put a second memory latency in front of every tile. The ping-pong loop's ring is described in its
+  // branch.
   Epi epi;
   const int nbase = n0 + wn * (BN / 2), mbase = m0 + wm * (BM / WMW);
   if constexpr (PP) {
