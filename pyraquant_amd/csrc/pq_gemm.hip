@@ -7,7 +7,8 @@
 //
 // Operand roles. The MFMA computes D = W_tile * A_tile^T: its row operand ("i") is a weight row n and its
 // column operand ("j") an activation row m, so each lane ends up holding 4 consecutive n of one output
-// row m (8-byte 16-bit stores) and needs one s_row value per 32 x 32 tile.
+// row m (8-byte 16-bit stores) and needs one s_row value per 32 x 32 tile. Group-32 without a low-rank term swaps
+// the two (each lane holds one column n and needs one group scale per tile; see the main loop).
 //
 // The kernel (gemm_dma_kernel). 2 x WMW wavefronts (WMW = 2 or 4 along m). A workgroup owns a BN x BM (n x m)
 // block, each wave a (BN/2) x (BM/WMW) part held as TI x TJ v_mfma_i32_32x32x32_i8 tiles (int32 accumulators in
@@ -30,7 +31,8 @@
 // (one MFMA from zero) the VALU converts and fma's with s_w[g, n] into an fp32 accumulator held in VGPRs, groups in
 // order. The scales of each stage ride the DMA ring (dword LDS-DMA, a ring of NS + 1 slots of their own). That is
 // 16 converts + 16 FMAs per lane per MFMA (128 VALU cycles of a wave64 against 32 of the MFMA), so group-32 is
-// VALU-bound at a quarter of the INT8 MFMA rate; blocks are 128 x 128 at two workgroups per CU.
+// VALU-bound at a quarter of the INT8 MFMA rate; blocks are 128 x 128 at two workgroups per CU (128 x 64 for small
+// problems and with a low-rank term).
 //
 // Workgroup ids are remapped so that each XCD (ids are dealt round-robin over the 8 XCDs) walks a contiguous
 // run of tiles, rasterised in groups of group_m() m-tiles for L2 reuse. Large 256 x 256 products run one persistent
