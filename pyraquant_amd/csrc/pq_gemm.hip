@@ -341,8 +341,10 @@ struct Epilogue {
   static constexpr int kRowBytes = 64 * TI;
   static constexpr int kPitch = kRowBytes + 16;
   static constexpr int kStageBytes = 32 * TJ * kPitch + 32 * TJ * 4;   // + the rows' scatter targets
+  static constexpr int kPitch32 = 64 * 4 + 16;   // int32 mode: a staged row of two weight tiles' outputs, padded
 
-  // Epilogue. int32 mode: the accumulators are stored straight from the fragments. Dequant modes: each fragment is
+  // Epilogue. int32 mode: the accumulators go through the wave's LDS staging area two weight tiles at a time and
+  // out as whole rows. Dequant modes: each fragment is
   // dequantized (+ low rank, + bias) and rounded in registers, written to the wave's LDS staging area in row-major
   // order, and the wave then stores whole rows: lane l writes 16 bytes, 4 TI lanes cover a row's 64 TI bytes, so
   // every store instruction writes complete 128-byte lines (the fragment layout alone would write 16-byte pieces
@@ -353,20 +355,31 @@ struct Epilogue {
     const int khalf = lane >> 5;
     const bool has_bias = p.bias != nullptr;
     if constexpr (MODE == kModeI32) {
+      // Two weight tiles (32 rows x 64 int32 outputs) per pass through the staging area, then whole rows out: 16
+      // lanes cover a row's 256 bytes, so each store instruction writes 4 rows of two complete 128-byte lines (the
+      // fragments alone would write 32 rows x 32 bytes per instruction).
+      static_assert(TI % 2 == 0 && 32 * kPitch32 <= kStageBytes, "int32 staging: pairs of weight tiles");
+      const int lr4 = lane >> 4, lc16 = lane & 15;
 #pragma unroll
-      for (int i = 0; i < TI; ++i) {
-        const int ntile = nbase + i * 32;
-        if (ntile >= p.N) continue;
-        const int nb = ntile + 4 * khalf;
+      for (int j = 0; j < TJ; ++j) {
 #pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-          const int m = mbase + j * 32 + (lane & 31);
-          if (m < p.M) {
-            int32_t* crow = static_cast<int32_t*>(p.c) + (int64_t)m * p.ldc;
-            const v16i& v = acc[i][j];
+        for (int ih = 0; ih < TI / 2; ++ih) {
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii) {
+            const v16i& v = acc[2 * ih + ii][j];
+            // fragment -> staging row lane % 32, outputs 32 ii + 8 q + 4 (lane / 32) .. + 3
+            uint8_t* const dst = stage + (lane & 31) * kPitch32 + (ii * 32 + 4 * khalf) * 4;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              *reinterpret_cast<v4i*>(crow + nb + 8 * q) = v4i{v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+              *reinterpret_cast<v4i*>(dst + 32 * q) = v4i{v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+          }
+          const int n = nbase + ih * 64 + lc16 * 4;
+#pragma unroll
+          for (int s0 = 0; s0 < 32; s0 += 4) {
+            const v4i v = *reinterpret_cast<const v4i*>(stage + (s0 + lr4) * kPitch32 + lc16 * 16);
+            const int m = mbase + j * 32 + s0 + lr4;
+            if (m < p.M && n < p.N)
+              *reinterpret_cast<v4i*>(static_cast<int32_t*>(p.c) + (int64_t)m * p.ldc + n) = v;
           }
           __builtin_amdgcn_sched_barrier(0);
         }
