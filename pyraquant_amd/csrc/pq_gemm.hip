@@ -581,8 +581,9 @@ void gemm_dma_kernel(const GemmArgs p) {
   // Persistent blocks: alternate rounds of an XCD's tiles (round = local index / workgroups per XCD) sweep K in
   // opposite directions. The raster's consecutive rounds share their m-tiles' A rows, so a reversed round starts on
   // the K range the previous round read last, which is still in the L2: 15 % fewer bytes fetched beyond the L2 at
-  // c1 (3.79 -> 3.23 GB), the same time. The int32 sums do not depend on the order.
-  const bool rev = PERSIST && (((vb >> 3) / max(1, (int)(gridDim.x >> 3))) & 1);
+  // c1 (3.79 -> 3.23 GB), the same time. The int32 sums do not depend on the order; group-32's fp32 sum over the
+  // groups does (and its scale DMA follows kt), so it always sweeps forward.
+  const bool rev = PERSIST && !G32 && (((vb >> 3) / max(1, (int)(gridDim.x >> 3))) & 1);
 
   // Buffer resources based at the block's first row. Rows past M / N, and the DMA of a stage past the end of K
   // (offset kOOB), lie outside num_records: those loads read no memory.
