@@ -493,6 +493,7 @@ class Int8Linear(nn.Module):
     _FP32_BUFFERS = ("w_scale", "w_scale_gn", "bias")
 
     def _apply(self, fn, recurse=True):
+        self.__dict__.pop("_direct_plans", None)   # (they hold the old buffers)
         keep = {n: self._buffers[n] for n in self._FP32_BUFFERS if self._buffers.get(n) is not None}
         super()._apply(fn, recurse)
         for n, old in keep.items():
@@ -527,45 +528,74 @@ class Int8Linear(nn.Module):
             return self.lr_Bt.to(dtype)
         return self.lr_Bt
 
+    # The tensors the direct call reads through raw pointers, looked up as nn.Module resolves attributes (instance
+    # dict first, then the registered buffers) without its __getattr__: a replaced, moved or re-registered one
+    # changes this tuple's identities and rebuilds the call's plan.
+    _DIRECT_SOURCES = ("weight_packed", "w_scale", "w_scale_gn", "bias", "lr_A", "lr_At", "lr_Bt")
+
+    def _direct_sources(self) -> tuple:
+        d, b = self.__dict__, self._buffers
+        return tuple(d[n] if n in d else b.get(n) for n in self._DIRECT_SOURCES) + (self._lr_frag(), self.group_size)
+
+    def _direct_plan(self, dt: torch.dtype, src: tuple):
+        """The part of the direct call that depends on the module alone, for input dtype dt: (source ids, the
+        sources themselves (kept alive, so their ids stay theirs), device, dtype code, R, the static C arguments),
+        or None where the direct path does not apply to this module and dtype."""
+        code = _DIRECT_DTYPES.get(dt)
+        wp, w_scale, w_scale_gn, bias, lr_A, lr_At, lr_Bt, frag, group = src
+        if code is None or wp is None:
+            return None
+        if lr_A is not None and (lr_At is None or lr_Bt is None):
+            return None
+        R = 0 if lr_At is None else lr_At.shape[0]          # columns of t
+        Re = 0 if lr_Bt is None else lr_Bt.shape[1]         # rank of the epilogue
+        if R and (lr_At.dtype != dt or lr_Bt.dtype != dt):
+            return None
+        # the GEMM reads these as fp32 through raw pointers: anything else goes to the general path, which asserts
+        sk = w_scale_gn if group else w_scale
+        dev = wp.device
+        if sk is None or sk.dtype != torch.float32 or sk.device != dev or not sk.is_contiguous():
+            return None
+        if bias is not None and (bias.dtype != torch.float32 or bias.device != dev):
+            return None
+        args = (wp.data_ptr(), sk.data_ptr(), group, None if bias is None else bias.data_ptr(),
+                lr_At.data_ptr() if R else None, frag.data_ptr() if R and frag is not None else None,
+                R, lr_Bt.data_ptr() if R else None, Re)
+        return tuple(map(id, src)), src, dev, code, R, args
+
     def _forward_direct(self, x: torch.Tensor) -> Optional[torch.Tensor]:
         """The common layer call (no routing arguments, packed weights) with the host work cut to one C call,
         pq_int8_linear: codes, scales and t share one workspace allocation, operands go as raw pointers, the stream
-        is the raw current stream. Same kernels and arguments as the general path, so the same bits; returns None
-        when a precondition of this path does not hold."""
+        is the raw current stream. What depends on the module alone (the checks of its buffers and their pointers)
+        is kept per input dtype and checked by identity on every call. Same kernels and arguments as the general
+        path, so the same bits; returns None when a precondition of this path does not hold."""
         dt = x.dtype
-        code = _DIRECT_DTYPES.get(dt)
+        src = self._direct_sources()
+        plans = self.__dict__.setdefault("_direct_plans", {})
+        plan = plans.get(dt)
+        if plan is None or plan[0] != tuple(map(id, src)):
+            plan = self._direct_plan(dt, src)
+            if plan is None:
+                return None
+            plans[dt] = plan
+        _, _, dev, code, R, args = plan
         K, N = self.in_features, self.out_features
-        if code is None or x.device != self.weight_packed.device or x.shape[-1] != K:
+        if x.shape[-1] != K or x.device != dev:
             return None
-        x2 = x.reshape(-1, K)
-        if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
-            return None
-        if self.lr_A is not None and (self.lr_At is None or self.lr_Bt is None):
-            return None
-        R = 0 if self.lr_At is None else self.lr_At.shape[0]          # columns of t
-        Re = 0 if self.lr_Bt is None else self.lr_Bt.shape[1]         # rank of the epilogue
-        if R and (self.lr_At.dtype != dt or self.lr_Bt.dtype != dt):
-            return None
-        frag = self._lr_frag()
-        # the GEMM reads these as fp32 through raw pointers: anything else goes to the general path, which asserts
-        sk = self._scale_k()
-        if sk.dtype != torch.float32 or sk.device != x.device or not sk.is_contiguous():
-            return None
-        if self.bias is not None and (self.bias.dtype != torch.float32 or self.bias.device != x.device):
+        x2 = x if x.dim() == 2 else x.reshape(-1, K)
+        ldx = x2.stride(0)
+        xp = x2.data_ptr()
+        if x2.stride(1) != 1 or ldx % 8 or xp % 16:
             return None
         M = x2.shape[0]
-        dev = x2.device
         L = _lib.load()
         ws = torch.empty(L.pq_int8_linear_workspace_size(M, K, R), dtype=torch.uint8, device=dev)
         out = torch.empty((M, N), dtype=dt, device=dev)
-        st = L.pq_int8_linear(x2.data_ptr(), code, M, K, x2.stride(0), self.weight_packed.data_ptr(), sk.data_ptr(),
-                              self.group_size, None if self.bias is None else self.bias.data_ptr(),
-                              self.lr_At.data_ptr() if R else None, frag.data_ptr() if R and frag is not None else None,
-                              R, self.lr_Bt.data_ptr() if R else None, Re,
-                              out.data_ptr(), N, N, ws.data_ptr(), ws.numel(), _raw_stream(dev))
+        st = L.pq_int8_linear(xp, code, M, K, ldx, *args, out.data_ptr(), N, N, ws.data_ptr(), ws.numel(),
+                              _raw_stream(dev))
         if st:
             _lib.check(st, "int8_linear")
-        return out.reshape(*x.shape[:-1], N)
+        return out if x.dim() == 2 else out.reshape(*x.shape[:-1], N)
 
     def forward(self, x: torch.Tensor, row_idx: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None, out_row_idx: Optional[torch.Tensor] = None,

@@ -300,6 +300,48 @@ def test_int8linear_direct_path_matches_general(cuda, K, N, R, group, dtype, M):
     assert torch.equal(y3.reshape(M, N), y_general)
 
 
+def test_direct_path_follows_buffer_changes(cuda):
+    """The direct path keeps the module's raw pointers per input dtype. Every way a buffer can change under it
+    (edited in place, replaced, removed, added to a layer built without it, lr_At repacked, a module-wide cast)
+    still gives the general path's bits on the next call."""
+    from pyraquant_amd import int8_exec as E
+    from pyraquant_amd.workloads import make_linear, make_x
+
+    def both(q, x):
+        y = q(x)
+        E.DIRECT_CALLS = False
+        try:
+            y_general = q(x)
+        finally:
+            E.DIRECT_CALLS = True
+        assert torch.equal(y, y_general)
+        return y
+
+    q = E.Int8Linear(make_linear(1280, 640, 32, True), device=cuda)
+    x = make_x(300, 1280, seed=3).to(cuda)
+    y0 = both(q, x)
+    assert "_direct_plans" in q.__dict__                      # the direct path ran and kept its plan
+    q.w_scale.mul_(2.0)                                         # in place: same pointer, new values
+    y1 = both(q, x)
+    assert not torch.equal(y1, y0)
+    q.w_scale = q.w_scale * 0.5                                 # a new tensor in the buffer's place
+    assert torch.equal(both(q, x), y0)
+    q.bias = None                                               # the buffer removed
+    y2 = both(q, x)
+    assert not torch.equal(y2, y0)
+    q.lr_At.mul_(0.0)                                           # in place: lr_At's fragment copy is repacked
+    y3 = both(q, x)
+    assert not torch.equal(y3, y2)
+    q.half()                                                    # a cast: 16-bit operands, fp32 scales kept
+    both(q, x.half())
+
+    p = E.Int8Linear(make_linear(640, 640, 0, False), device=cuda)
+    xb = make_x(64, 640, seed=4).to(cuda)
+    z0 = both(p, xb)
+    p.bias = torch.full((640,), 0.25, device=cuda)              # added to a layer built without one
+    assert not torch.equal(both(p, xb), z0)
+
+
 def test_int8linear_graph_replay(cuda):
     """A chain of Int8Linear forwards captured in a HIP graph (torch.cuda.graph) replays to the eager bits, replay
     after replay, with eager work and synchronisation between replays: the kernels allocate and clear nothing
