@@ -178,6 +178,25 @@ def main() -> int:
     qa_bytes = 3.0 * M * cfg.K + 4.0 * M + (4.0 * M if rows is not None else 0.0)
     qa_gbs = qa_bytes / (qa_ms * 1e-3) / 1e9
 
+    # The low-rank down-projection alone (t = x[rows] @ L1 by the LDS-DMA kernel), the path of layers the fused
+    # quantizer pass does not take (other ranks, other K): x read once, L1^T, t written.
+    lowrank_alone = None
+    if q.lr_At is not None and x.dtype == q.lr_At.dtype:
+        for _ in range(3):
+            E.lowrank_down(x, q.lr_At, rows)
+        qe0.record()
+        for _ in range(10):
+            E.lowrank_down(x, q.lr_At, rows)
+        qe1.record()
+        torch.cuda.synchronize()
+        la_ms = qe0.elapsed_time(qe1) / 10
+        rd = q.lr_At.shape[0]
+        la_bytes = 2.0 * M * cfg.K + 2.0 * rd * cfg.K + 2.0 * M * rd + (4.0 * M if rows is not None else 0.0)
+        lowrank_alone = {"kernel": "lowrank_down", "us": round(la_ms * 1e3, 1),
+                         "GBps": round(la_bytes / (la_ms * 1e-3) / 1e9, 1),
+                         "frac_hbm": round(la_bytes / (la_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "bytes": "2 M K + 2 R K + 2 M R"}
+
     # HBM bytes per GEMM launch measured by rocprofv3 (FETCH_SIZE + WRITE_SIZE, copy-calibrated) for this config
     traffic, traffic_src = None, None
     prof = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", f"int8_gemm_{cfg.name}_traffic.json")
@@ -225,7 +244,8 @@ def main() -> int:
             "quantizer_alone": {"kernel": "quant_rows_packed", "us": round(qa_ms * 1e3, 1),
                                 "GBps": round(qa_gbs, 1), "frac_hbm": round(qa_gbs / HBM_PEAK_GBS, 4),
                                 "bytes": f"3 M K + 4 M{' + 4 M (gather list)' if rows is not None else ''}"},
-        } | ({"routing": routing} if routing is not None else {}) | ({"small_m_launch": launch} if launch else {}) | ({"weight_fold": fold} if fold else {}) | ({"flux_linear_mix": mix} if mix else {}),
+        } | ({"lowrank_down_alone": lowrank_alone} if lowrank_alone else {})
+          | ({"routing": routing} if routing is not None else {}) | ({"small_m_launch": launch} if launch else {}) | ({"weight_fold": fold} if fold else {}) | ({"flux_linear_mix": mix} if mix else {}),
         "roofline": {
             "bound": "mfma",
             "achieved": round(gemm_tops, 2),
