@@ -313,8 +313,6 @@ __global__ __launch_bounds__(256) void pack_k64_kernel(const int8_t* __restrict_
 constexpr int kLrRows = 128;
 constexpr int kLrNS = 4;
 
-__device__ __forceinline__ int lr_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-
 template <int DT, int RB>
 __global__ __launch_bounds__(256) void lowrank_down_dma_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int64_t x_rows, int K, int64_t M, const int32_t* __restrict__ row_idx,
@@ -711,7 +709,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void quant_lowrank_wide_kernel(
   bool live[RPW];
 #pragma unroll
   for (int rho = 0; rho < RPW; ++rho) live[rho] = false;
-  if (blockIdx.x < nbatch) {
+  if ((int)blockIdx.x < nbatch) {
 #pragma unroll
     for (int rho = 0; rho < RPW; ++rho) {
       live[rho] = src_of(blockIdx.x, rho) >= 0;

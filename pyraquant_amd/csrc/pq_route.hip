@@ -121,7 +121,7 @@ __global__ __launch_bounds__(256) void route_union_kernel(const uint8_t* __restr
       base += tot;
     }
   }
-  if (blockIdx.x == G - 1 && threadIdx.x == 0) count[0] = base;
+  if ((int)blockIdx.x == G - 1 && threadIdx.x == 0) count[0] = base;
 }
 
 // ---- patch table (flux/run_flux.py:340-355 boxes, flux/routing.py:202-315 cores / halos / order) --------------------
